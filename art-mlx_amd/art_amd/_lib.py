@@ -1,0 +1,112 @@
+"""ctypes binding of libart_moe.so (the C ABI declared in include/art_moe.h).
+
+This is the whole Python <-> native boundary: plain pointers, sizes and a
+hipStream_t, no torch types.  torch is imported before the library is loaded
+so that libart_moe binds to the HIP runtime torch already loaded (same SONAME,
+libamdhip64.so.7); device pointers and streams are then shared.
+
+There is no CPU fallback: if the library is missing every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must load torch's HIP runtime first)
+
+LIB_PATH = Path(__file__).with_name("libart_moe.so")
+
+ART_MOE_OK = 0
+ART_MOE_ERR_INVALID_ARG = -1
+ART_MOE_ERR_UNSUPPORTED = -2
+ART_MOE_ERR_HIP = -3
+SEG_NBM = 4
+
+
+def seg_len(num_experts: int) -> int:
+    return (1 + SEG_NBM) * (num_experts + 1)
+
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/art_moe.h exactly.
+SIGNATURES = {
+    "art_moe_version": (_I32, []),
+    "art_moe_last_error": (ctypes.c_char_p, []),
+    "art_moe_router_topk": (_I32, [_P, _I64, _I32, _I32, _P, _P, _P]),
+    "art_moe_router_replay": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "art_moe_router_backward": (_I32, [_P, _I32, _I64, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
+    "art_moe_plan_workspace_bytes": (_SZ, [_I64, _I32]),
+    "art_moe_dispatch_plan": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "art_moe_segments_from_counts": (_I32, [_P, _I32, _P, _P]),
+    "art_moe_permute": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P]),
+    "art_moe_combine": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _P]),
+    "art_moe_grouped_gemm": (_I32, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I32,
+                                    _P, _I32, _I64, _I32, _I32, _F, _P, _I64, _I32, _P]),
+    "art_moe_fc1_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _I32, _P, _I32, _I64, _I32,
+                                  _I32, _P, _P, _P, _P]),
+    "art_moe_dgrad_swiglu_parts": (_I32, [_I32]),
+    "art_moe_fc2_dgrad_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _I32, _P, _I32, _I64,
+                                        _I32, _I32, _P, _P, _P, _P, _P]),
+    "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I32, _I32, _F, _P,
+                                     _I64, _I64, _I64, _I32, _P]),
+    "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
+}
+
+
+class ArtMoeError(RuntimeError):
+    """A libart_moe call failed (HIP error or unsupported configuration)."""
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libart_moe.so once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ArtMoeError(
+                    f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+                    "g.build()'` (hipcc, gfx950).  There is no CPU fallback.")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args):
+    """Call ``name`` and turn a non-zero status into an exception.
+
+    ART_MOE_ERR_INVALID_ARG becomes ValueError (the reference operator raises
+    ValueError for invalid arguments); anything else ArtMoeError.
+    """
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != ART_MOE_OK:
+        msg = lib.art_moe_last_error().decode(errors="replace")
+        if rc == ART_MOE_ERR_INVALID_ARG:
+            raise ValueError(f"{name}: {msg}")
+        raise ArtMoeError(f"{name} failed ({rc}): {msg}")
+    return rc
+
+
+def stream_ptr(device: torch.device | None = None) -> int:
+    """hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,185 @@
+"""The MoE-LoRA expert layer on gfx950, forward and backward.
+
+Computes what megatron's MoELayer does for ART's LoRA-trained experts
+(router -> token dispatch -> TEGroupedMLP with MLPExpertsLinearFC1LoRA /
+weighted SwiGLU / MLPExpertsLinearFC2LoRA -> combine; reference call stack
+/root/reference/src/art/megatron/lora.py:1464-1571,
+/root/reference/src/art/megatron/compile_workarounds.py:73-106,
+/root/reference/src/art/megatron/runtime/bridge_runtime.py:775-900), as a
+sequence of HIP kernels:
+
+forward
+  1 router gating linear  logits = x W_r^T (fp32 accumulate)    [or given logits]
+  2 top-k softmax          idx, w                               [or replay target]
+  3 dispatch plan          counts, segment table, dest, row->token, row->prob
+  4 LoRA projection        t1 = x[row] [A_g | A_u]               (rows gathered)
+  5 FC1 + LoRA + SwiGLU    y1 = x[row] W1^T + t1 L1^T ; h = silu(g) u p
+  6 LoRA projection        t2 = h A_d
+  7 FC2 + LoRA             y2 = h W2^T + t2 (s_d B_d)^T
+  8 combine                y[t] = sum_j y2[dest[t, j]]
+backward
+  1 g2  = s_d dy[row] B_d^T
+  2 FC2 dgrad + SwiGLU bwd dy1, dp  (dh = dy[row] W2 + g2 A_d^T)
+  3 g1  = [s_g dg B_g^T | s_u du B_u^T]
+  4 FC1 dgrad              dx_perm = dy1 W1 + g1 [A_g | A_u]^T
+  5 router bwd             dl = w (dw - <w, dw>)
+  6 un-permute + router dx dx[t] = sum_j dx_perm[dest[t,j]] + sum_j dl[t,j] W_r[idx[t,j]]
+  7 LoRA weight grads      segmented fp32 TN products
+The permuted activations x[row] and dy[row] are never materialised: the
+GEMMs gather rows through row_token on load.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from ... import ops
+from ..kernels.grouped_lora_hip import apply_operand, pad_rank_last, pad_rank_mid, padded_rank, proj_operand
+
+
+@dataclass
+class FrozenExperts:
+    """Frozen base weights plus their transposed copies (built once).
+
+    w_r [E, H] router weight (None when the caller supplies logits)
+    w1  [E, 2F, H] FC1 (TE GroupedLinear ``weight{e}`` layout, gate rows first)
+    w2  [E, H, F]  FC2
+    w1t [E, H, 2F], w2t [E, F, H] transposed copies for the data gradients.
+    """
+    w_r: torch.Tensor | None
+    w1: torch.Tensor
+    w2: torch.Tensor
+    w1t: torch.Tensor
+    w2t: torch.Tensor
+
+    @classmethod
+    def build(cls, w_r, w1, w2) -> "FrozenExperts":
+        w1 = w1.detach().contiguous()
+        w2 = w2.detach().contiguous()
+        return cls(w_r.detach().contiguous() if w_r is not None else None,
+                   w1, w2, ops.transposed(w1), ops.transposed(w2))
+
+    @property
+    def num_experts(self) -> int:
+        return self.w1.shape[0]
+
+    @property
+    def hidden(self) -> int:
+        return self.w1.shape[2]
+
+    @property
+    def ffn(self) -> int:
+        return self.w1.shape[1] // 2
+
+
+def _single_segment(num_rows: int, device) -> torch.Tensor:
+    counts = torch.full((1,), num_rows, dtype=torch.int64, device=device)
+    return ops.segments_from_counts(counts, 1, device)
+
+
+def router_logits(x: torch.Tensor, w_r: torch.Tensor) -> torch.Tensor:
+    """logits = x.float() @ W_r.float().T on bf16 MFMA with fp32 accumulation
+    (products of bf16 values are exact in fp32)."""
+    t = x.shape[0]
+    seg = _single_segment(t, x.device)
+    return ops.grouped_gemm(x, w_r.unsqueeze(0), seg, 1, m=t, out_fp32=True)
+
+
+class _MoELoRALayerFn(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, base: FrozenExperts,
+                k: int, scales: tuple[float, float, float]):
+        e, h_dim, f = base.num_experts, base.hidden, base.ffn
+        sg, su, sd = scales
+        x = x.contiguous()
+        t = x.shape[0]
+        logits_supplied = logits is not None
+        if not logits_supplied:
+            logits = router_logits(x, base.w_r)
+        if target is None:
+            idx, w = ops.router_topk(logits, k)
+            status = None
+        else:
+            idx, w, status = ops.router_replay(logits, target)
+        plan = ops.dispatch_plan(idx, w, e, status=status)
+        m = t * k
+        rows = plan.row_token
+        rg, ru, rd = a_g.shape[-1], a_u.shape[-1], a_d.shape[-1]
+        rpg, rpu, rpd = padded_rank(rg), padded_rank(ru), padded_rank(rd)
+        # LoRA operand layouts (tiny; rebuilt every call since the factors train)
+        a1p = proj_operand([a_g, a_u], [rpg, rpu])                 # [E, RPg+RPu, H]
+        l1 = a_g.new_zeros((e, 2 * f, rpg + rpu))                 # [E, 2F, RPg+RPu]
+        ops.transpose_into(b_g, l1[:, :f, :rg], sg)
+        ops.transpose_into(b_u, l1[:, f:, rpg:rpg + ru], su)
+        t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
+        y1, h = ops.fc1_swiglu(x, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
+                               tl=t1, l1=l1)
+        t2 = ops.grouped_gemm(h, proj_operand([a_d], [rpd]), plan.seg, e, m=m)
+        y2 = ops.grouped_gemm(h, base.w2, plan.seg, e, m=m, tl=t2, l=apply_operand(b_d, rpd, sd))
+        y = ops.combine(y2, plan.dest, t)
+        ctx.save_for_backward(x, idx, w, plan.dest, rows, plan.row_prob, plan.seg, t1, y1, h, t2,
+                              a_g, b_g, a_u, b_u, a_d, b_d)
+        ctx.base = base
+        ctx.meta = (k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd)
+        ctx.logits_supplied = logits_supplied
+        ctx.mark_non_differentiable(idx, plan.counts, plan.status)
+        return y, idx, plan.counts, plan.status
+
+    @staticmethod
+    def backward(ctx, dy, *unused: Any):
+        (x, idx, w, dest, rows, row_prob, seg, t1, y1, h, t2,
+         a_g, b_g, a_u, b_u, a_d, b_d) = ctx.saved_tensors
+        base: FrozenExperts = ctx.base
+        k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd = ctx.meta
+        e, f = base.num_experts, base.ffn
+        t = x.shape[0]
+        m = t * k
+        dy = dy.contiguous()
+        # FC2 data gradient with the SwiGLU backward in its epilogue
+        g2 = ops.grouped_gemm(dy, pad_rank_mid(b_d, rpd), seg, e, m=m, a_rows=rows, alpha=sd)
+        dy1, dp_part = ops.fc2_dgrad_swiglu(dy, base.w2t, seg, e, y1, row_prob, m=m, a_rows=rows,
+                                            tl=g2, l2=pad_rank_last(a_d, rpd))
+        # g1 = [s_g dg B_g^T | s_u du B_u^T] as one product (dy1 read once) with
+        # the block-diagonal operand [[s_g B_g, 0], [0, s_u B_u]]
+        gb = b_g.new_zeros((e, rpg + rpu, 2 * f))
+        gb[:, :rg, :f] = b_g * sg
+        gb[:, rpg:rpg + ru, f:] = b_u * su
+        g1 = ops.grouped_gemm(dy1, gb, seg, e, m=m)
+        a1cat = torch.cat((pad_rank_last(a_g, rpg), pad_rank_last(a_u, rpu)), dim=-1)
+        dx_perm = ops.grouped_gemm(dy1, base.w1t, seg, e, m=m, tl=g1, l=a1cat)
+        # router: softmax backward over the k selected logits
+        dl, dlogits = ops.router_backward(dp_part, dest, w, idx, e,
+                                          dense=ctx.logits_supplied and ctx.needs_input_grad[1])
+        if not ctx.logits_supplied:
+            dx = ops.combine(dx_perm, dest, t, dl=dl, idx=idx, w_r=base.w_r)
+        else:
+            dx = ops.combine(dx_perm, dest, t)
+        # LoRA weight gradients (fp32 accumulation, returned in parameter dtype)
+        da1 = ops.grouped_wgrad(x, g1, seg, e, l_rows=rows)                          # [E,H,RP1]
+        dbg = ops.grouped_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, alpha=sg, transpose_out=True)
+        dbu = ops.grouped_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, alpha=su, transpose_out=True)
+        dad = ops.grouped_wgrad(h, g2, seg, e)                                        # [E,F,RPd]
+        dbd = ops.grouped_wgrad(dy, t2, seg, e, alpha=sd, l_rows=rows, transpose_out=True)
+        return (dx, dlogits, None,
+                da1[:, :, :rg].to(a_g.dtype), dbg[:, :rg].to(b_g.dtype),
+                da1[:, :, rpg:rpg + ru].to(a_u.dtype), dbu[:, :ru].to(b_u.dtype),
+                dad[:, :, :rd].to(a_d.dtype), dbd[:, :rd].to(b_d.dtype),
+                None, None, None)
+
+
+def moe_lora_layer(x, base: FrozenExperts, a_g, b_g, a_u, b_u, a_d, b_d, *, k: int,
+                   scales: tuple[float, float, float], logits: torch.Tensor | None = None,
+                   target: torch.Tensor | None = None):
+    """Functional layer.  Returns (y [T,H] bf16, idx [T,k], counts [E], status [1]).
+
+    ``logits`` (fp32 [T,E]) replaces the router gating linear; ``target``
+    (int [T,k]) replays routes.  ``status`` counts rejected replay ids.
+    """
+    if x.dtype != torch.bfloat16 or x.device.type != "cuda":
+        raise ValueError("x must be a bf16 CUDA tensor")
+    if logits is None and base.w_r is None:
+        raise ValueError("either router weights or logits are required")
+    return _MoELoRALayerFn.apply(x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, base, k, scales)

@@ -1,0 +1,277 @@
+"""Tensor-level wrappers of the libart_moe C ABI.
+
+Each function takes torch CUDA tensors, checks shapes/dtypes on the host,
+allocates outputs with torch (device memory only), and launches on torch's
+current stream.  No function synchronizes with the host.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, stream_ptr
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _cuda(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("libart_moe ops need CUDA (HIP) tensors")
+
+
+def _rowmajor(t: torch.Tensor, name: str) -> int:
+    """Leading dimension of a 2-D (or [E,R,C]) tensor whose last dim is contiguous."""
+    _need(t.stride(-1) == 1, f"{name} must have a contiguous last dimension")
+    return t.stride(-2) if t.dim() >= 2 else t.shape[-1]
+
+
+# ------------------------------------------------------------------ routing
+def router_topk(logits: torch.Tensor, k: int):
+    """Top-k softmax routing.  Returns (idx int32 [T,k], w fp32 [T,k])."""
+    _cuda(logits)
+    _need(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be fp32 [T, E]")
+    logits = logits.contiguous()
+    t, e = logits.shape
+    idx = torch.empty((t, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    call("art_moe_router_topk", ptr(logits), t, e, k, ptr(idx), ptr(w), stream_ptr(logits.device))
+    return idx, w
+
+
+def router_replay(logits: torch.Tensor, target: torch.Tensor, status: torch.Tensor | None = None):
+    """Replay ``target`` [T,k] ids.  Returns (idx, w, status); status counts rejected ids."""
+    _cuda(logits, target)
+    _need(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be fp32 [T, E]")
+    _need(target.dim() == 2 and target.shape[0] == logits.shape[0], "target must be [T, k]")
+    logits = logits.contiguous()
+    target = target.to(torch.int64).contiguous()
+    t, e = logits.shape
+    k = target.shape[1]
+    idx = torch.empty((t, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    if status is None:
+        status = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    call("art_moe_router_replay", ptr(logits), ptr(target), t, e, k, ptr(idx), ptr(w), ptr(status),
+         stream_ptr(logits.device))
+    return idx, w, status
+
+
+def router_backward(dp_part: torch.Tensor, dest: torch.Tensor, w: torch.Tensor,
+                    idx: torch.Tensor, num_experts: int, dense: bool = False):
+    """(dl [T,k], dlogits [T,E] or None) from partial dL/dp vectors [n_part, M]."""
+    _cuda(dp_part, dest, w, idx)
+    t, k = w.shape
+    n_part, m = (dp_part.shape if dp_part.numel() else (0, 0))
+    dl = torch.empty((t, k), dtype=torch.float32, device=w.device)
+    dlogits = torch.empty((t, num_experts), dtype=torch.float32, device=w.device) if dense else None
+    call("art_moe_router_backward", ptr(dp_part), n_part, m, ptr(dest), ptr(w), ptr(idx), t,
+         num_experts, k, ptr(dl), ptr(dlogits), stream_ptr(w.device))
+    return dl, dlogits
+
+
+@dataclass
+class DispatchPlan:
+    """Device-side dispatch plan (see art_moe_dispatch_plan)."""
+    counts: torch.Tensor     # int32 [E]
+    seg: torch.Tensor        # int32 [SEG_LEN(E)]
+    dest: torch.Tensor       # int32 [T,k]
+    row_token: torch.Tensor  # int32 [M]
+    row_prob: torch.Tensor | None  # fp32 [M]
+    status: torch.Tensor     # int32 [1]
+    num_experts: int
+
+    @property
+    def offsets(self) -> torch.Tensor:
+        return self.seg[: self.num_experts + 1]
+
+
+def dispatch_plan(idx: torch.Tensor, w: torch.Tensor | None, num_experts: int,
+                  status: torch.Tensor | None = None) -> DispatchPlan:
+    _cuda(idx, w)
+    _need(idx.dtype == torch.int32 and idx.dim() == 2, "idx must be int32 [T, k]")
+    idx = idx.contiguous()
+    t, k = idx.shape
+    dev = idx.device
+    counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
+    seg = torch.empty(_lib.seg_len(num_experts), dtype=torch.int32, device=dev)
+    dest = torch.empty((t, k), dtype=torch.int32, device=dev)
+    row_token = torch.empty(t * k, dtype=torch.int32, device=dev)
+    row_prob = torch.empty(t * k, dtype=torch.float32, device=dev) if w is not None else None
+    if status is None:
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws_bytes = int(_lib.load().art_moe_plan_workspace_bytes(t, num_experts))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    wc = w.contiguous() if w is not None else None
+    call("art_moe_dispatch_plan", ptr(idx), ptr(wc), t, num_experts, k, ptr(counts), ptr(seg),
+         ptr(dest), ptr(row_token), ptr(row_prob), ptr(status), ptr(ws), ws_bytes, stream_ptr(dev))
+    return DispatchPlan(counts, seg, dest, row_token, row_prob, status, num_experts)
+
+
+def segments_from_counts(counts, num_experts: int, device) -> torch.Tensor:
+    """Segment table from tokens_per_expert (list or tensor, host or device)."""
+    if isinstance(counts, torch.Tensor):
+        c = counts.detach().to(device=device, dtype=torch.int64).contiguous()
+    else:
+        c = torch.tensor([int(v) for v in counts], dtype=torch.int64, device=device)
+    _need(c.numel() == num_experts, "counts length must equal the number of experts")
+    seg = torch.empty(_lib.seg_len(num_experts), dtype=torch.int32, device=device)
+    call("art_moe_segments_from_counts", ptr(c), num_experts, ptr(seg), stream_ptr(seg.device))
+    return seg
+
+
+# ---------------------------------------------------------- permute/combine
+def permute(x: torch.Tensor, dest: torch.Tensor, num_rows: int) -> torch.Tensor:
+    _cuda(x, dest)
+    _need(x.dtype == torch.bfloat16 and x.dim() == 2, "x must be bf16 [T, H]")
+    x = x.contiguous()
+    t, h = x.shape
+    out = torch.empty((num_rows, h), dtype=x.dtype, device=x.device)
+    call("art_moe_permute", ptr(x), ptr(dest.contiguous()), t, dest.shape[1], h, ptr(out),
+         stream_ptr(x.device))
+    return out
+
+
+def combine(y_perm: torch.Tensor, dest: torch.Tensor, num_tokens: int, *,
+            wgt: torch.Tensor | None = None, dl: torch.Tensor | None = None,
+            idx: torch.Tensor | None = None, w_r: torch.Tensor | None = None) -> torch.Tensor:
+    _cuda(y_perm, dest, wgt, dl, idx, w_r)
+    _need(y_perm.dtype == torch.bfloat16 and y_perm.dim() == 2, "y_perm must be bf16 [M, H]")
+    y_perm = y_perm.contiguous()
+    h = y_perm.shape[1]
+    y = torch.empty((num_tokens, h), dtype=y_perm.dtype, device=y_perm.device)
+    if w_r is not None:
+        _need(w_r.dtype == torch.bfloat16 and w_r.shape[1] == h, "w_r must be bf16 [E, H]")
+        w_r = w_r.contiguous()
+    call("art_moe_combine", ptr(y_perm), ptr(dest.contiguous()),
+         ptr(wgt.contiguous() if wgt is not None else None),
+         ptr(dl.contiguous() if dl is not None else None),
+         ptr(idx.contiguous() if idx is not None else None), ptr(w_r),
+         num_tokens, dest.shape[1], h, ptr(y), stream_ptr(y.device))
+    return y
+
+
+# ------------------------------------------------------------ grouped GEMM
+def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_experts: int, *,
+                 m: int | None = None, a_rows: torch.Tensor | None = None,
+                 tl: torch.Tensor | None = None, l: torch.Tensor | None = None,
+                 alpha: float = 1.0, out_fp32: bool = False,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = alpha * (A[row(m)] @ B[e]^T + Tl @ L[e]^T) per expert segment.
+
+    a [*, K] bf16; b [E, N, K] bf16 (last dim contiguous); tl [M, kt], l [E, N, kt].
+    """
+    _cuda(a, b, seg, a_rows, tl, l)
+    _need(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16, "A and B must be bf16")
+    _need(b.dim() == 3 and b.shape[0] == num_experts, "B must be [E, N, K]")
+    n, k = b.shape[1], b.shape[2]
+    _need(a.shape[-1] == k, f"A has K={a.shape[-1]}, B has K={k}")
+    if m is None:
+        m = a_rows.shape[0] if a_rows is not None else a.shape[0]
+    kt = 0
+    ldt = ldl = l_es = 0
+    if tl is not None:
+        kt = tl.shape[1]
+        _need(l is not None and l.shape == (num_experts, n, kt), "L must be [E, N, kt]")
+        _need(tl.dtype == torch.bfloat16 and l.dtype == torch.bfloat16, "LoRA operands must be bf16")
+        ldt, ldl, l_es = _rowmajor(tl, "Tl"), _rowmajor(l, "L"), l.stride(0)
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32 if out_fp32 else torch.bfloat16, device=a.device)
+    call("art_moe_grouped_gemm", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(b), _rowmajor(b, "B"),
+         b.stride(0), ptr(tl), ldt, ptr(l), ldl, l_es, kt, ptr(seg), num_experts, m, n, k,
+         float(alpha), ptr(out), _rowmajor(out, "C"), int(out.dtype == torch.float32),
+         stream_ptr(a.device))
+    return out
+
+
+def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts: int,
+               row_prob: torch.Tensor, *, m: int, a_rows: torch.Tensor | None = None,
+               tl: torch.Tensor | None = None, l1: torch.Tensor | None = None):
+    """(y1 [M,2F], h [M,F]) = FC1 (+LoRA) then weighted SwiGLU, fused."""
+    _cuda(a, w1, seg, row_prob, a_rows, tl, l1)
+    e, f2, k = w1.shape
+    f = f2 // 2
+    _need(w1.is_contiguous() and w1.dtype == torch.bfloat16, "w1 must be contiguous bf16 [E, 2F, K]")
+    kt = 0
+    ldt = 0
+    if tl is not None:
+        kt = tl.shape[1]
+        _need(l1 is not None and l1.shape == (e, f2, kt) and l1.is_contiguous(), "L1 must be [E, 2F, kt]")
+        ldt = _rowmajor(tl, "Tl")
+    y1 = torch.empty((m, f2), dtype=torch.bfloat16, device=a.device)
+    h = torch.empty((m, f), dtype=torch.bfloat16, device=a.device)
+    call("art_moe_fc1_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w1), ptr(tl), ldt,
+         ptr(l1), kt, ptr(seg), num_experts, m, f, k, ptr(row_prob), ptr(y1), ptr(h),
+         stream_ptr(a.device))
+    return y1, h
+
+
+def dgrad_swiglu_parts(f: int) -> int:
+    return int(_lib.load().art_moe_dgrad_swiglu_parts(f))
+
+
+def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_experts: int,
+                     y1: torch.Tensor, row_prob: torch.Tensor, *, m: int,
+                     a_rows: torch.Tensor | None = None, tl: torch.Tensor | None = None,
+                     l2: torch.Tensor | None = None):
+    """(dy1 [M,2F] bf16, dp_part [n_parts, M] fp32) of the FC2 dgrad + SwiGLU backward."""
+    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2)
+    e, f, k = w2t.shape
+    _need(w2t.is_contiguous() and w2t.dtype == torch.bfloat16, "w2t must be contiguous bf16 [E, F, K]")
+    _need(y1.is_contiguous() and y1.shape == (m, 2 * f), "y1 must be contiguous [M, 2F]")
+    kt = 0
+    ldt = 0
+    if tl is not None:
+        kt = tl.shape[1]
+        _need(l2 is not None and l2.shape == (e, f, kt) and l2.is_contiguous(), "L2 must be [E, F, kt]")
+        ldt = _rowmajor(tl, "Tl")
+    dy1 = torch.empty((m, 2 * f), dtype=torch.bfloat16, device=a.device)
+    dp_part = torch.empty((dgrad_swiglu_parts(f), m), dtype=torch.float32, device=a.device)
+    call("art_moe_fc2_dgrad_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w2t), ptr(tl), ldt,
+         ptr(l2), kt, ptr(seg), num_experts, m, f, k, ptr(y1), ptr(row_prob), ptr(dy1),
+         ptr(dp_part), stream_ptr(a.device))
+    return dy1, dp_part
+
+
+def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_experts: int, *,
+                  alpha: float = 1.0, l_rows: torch.Tensor | None = None,
+                  r_rows: torch.Tensor | None = None, transpose_out: bool = False,
+                  out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """out[e] = alpha * Lm_e^T @ R_e (fp32 [E,P,Q]; [E,Q,P] with transpose_out)."""
+    _cuda(lm, r, seg, l_rows, r_rows, out)
+    p, q = lm.shape[-1], r.shape[-1]
+    if out is None:
+        shape = (num_experts, q, p) if transpose_out else (num_experts, p, q)
+        out = torch.empty(shape, dtype=torch.float32, device=lm.device)
+    _need(out.dtype == torch.float32, "wgrad output must be fp32")
+    if transpose_out:
+        o_es, o_ps, o_qs = out.stride(0), out.stride(2), out.stride(1)
+    else:
+        o_es, o_ps, o_qs = out.stride(0), out.stride(1), out.stride(2)
+    call("art_moe_grouped_wgrad", ptr(lm), _rowmajor(lm, "Lm"), ptr(l_rows), ptr(r), _rowmajor(r, "R"),
+         ptr(r_rows), ptr(seg), num_experts, p, q, float(alpha), ptr(out), o_es, o_ps, o_qs,
+         int(accumulate), stream_ptr(lm.device))
+    return out
+
+
+def transpose_into(src: torch.Tensor, dst: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """dst[e, c, r] = scale * src[e, r, c] for 3-D bf16 views with contiguous last dims."""
+    _cuda(src, dst)
+    _need(src.dim() == 3 and dst.dim() == 3, "transpose_into needs 3-D views")
+    e, r, c = src.shape
+    _need(dst.shape == (e, c, r), f"dst must be {(e, c, r)}, got {tuple(dst.shape)}")
+    _need(src.stride(2) == 1 and dst.stride(2) == 1, "last dims must be contiguous")
+    call("art_moe_transpose", ptr(src), e, r, c, src.stride(0), src.stride(1), ptr(dst),
+         dst.stride(0), dst.stride(1), float(scale), stream_ptr(src.device))
+    return dst
+
+
+def transposed(src: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    e, r, c = src.shape
+    dst = torch.empty((e, c, r), dtype=src.dtype, device=src.device)
+    return transpose_into(src, dst, scale)

@@ -1,0 +1,536 @@
+// Routing, dispatch plan, permute and combine kernels (bandwidth-bound family).
+//
+// Reference semantics (paths under the reference tree):
+//   top-k softmax routing   megatron TopKRouter.routing, contract in
+//                           tests/unit/test_moe_routing_replay.py:181-205,
+//                           restated in src/art/megatron/dsv4/layer.py:139-191
+//   routing replay          RouterReplay.get_replay_topk (fake at
+//                           tests/unit/test_moe_routing_replay.py:149-161)
+//   dispatch order          expert-major, token-ascending (megatron permute
+//                           with routing map; canonical order enforced at
+//                           tests/integration/megatron/routing_replay/trace.py:181-232)
+//   combine                 megatron moe_utils.unpermute (scatter-add of the k
+//                           expert rows of each token), signature at
+//                           src/art/megatron/runtime/bridge_runtime.py:870-879
+#include <math.h>
+
+#include "common.h"
+
+namespace art {
+
+// ---------------------------------------------------------------- top-k
+// Total order used for selection: NaN above every number, -0.0 == +0.0, and
+// among equal values the lower expert id first.  order_key maps a float to an
+// unsigned key that compares like the float; the 64-bit candidate key packs
+// (order_key << 32) | ~expert so that one unsigned max picks value then id.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  if (f != f) return 0xFFFFFFFFu;
+  uint32_t u = __float_as_uint(f);
+  if ((u << 1) == 0) u = 0;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t key) {
+  if (key == 0xFFFFFFFFu) return __uint_as_float(0x7fc00000u);
+  uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_xor(lo, o, kWave);
+  hi = __shfl_xor(hi, o, kWave);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl(lo, src, kWave);
+  hi = __shfl(hi, src, kWave);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// One wavefront per token row; lane l holds experts l, l+64, ... (EPL of them).
+template <int EPL>
+__global__ __launch_bounds__(256) void topk_softmax_kernel(
+    const float *__restrict__ logits, int64_t T, int E, int k,
+    int32_t *__restrict__ idx, float *__restrict__ w) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float *row = logits + t * (int64_t)E;
+  uint64_t cand[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + kWave * i;
+    cand[i] = (e < E) ? (((uint64_t)order_key(row[e]) << 32) | (uint32_t)(~(uint32_t)e)) : 0ull;
+  }
+  uint64_t mine = 0;
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) best = cand[i] > best ? cand[i] : best;
+    uint64_t wbest = best;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      uint64_t other = shfl_xor_u64(wbest, o);
+      wbest = other > wbest ? other : wbest;
+    }
+    // Keys are unique (they embed the id), so exactly one lane owns wbest.
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (cand[i] == wbest) cand[i] = 0ull;
+    if (lane == j) mine = wbest;
+  }
+  const bool act = lane < k;
+  const float v = act ? key_value((uint32_t)(mine >> 32)) : 0.0f;
+  const float vmax = __shfl(v, 0, kWave);  // first winner is the maximum
+  const float ex = act ? expf(v - vmax) : 0.0f;
+  const float s = wave_sum(ex);
+  if (act) {
+    idx[t * k + lane] = (int32_t)(~(uint32_t)mine);
+    w[t * k + lane] = ex / s;
+  }
+}
+
+// Replay: lane j < k of the token's wave takes target[t, j].
+__global__ __launch_bounds__(256) void replay_kernel(
+    const float *__restrict__ logits, const int64_t *__restrict__ target,
+    int64_t T, int E, int k, int32_t *__restrict__ idx, float *__restrict__ w,
+    int32_t *__restrict__ status) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const bool act = lane < k;
+  int64_t e = act ? target[t * k + lane] : -1;
+  bool valid = act && e >= 0 && e < E;
+  // Repeated id in a row: every later occurrence is rejected.
+  for (int j = 0; j < k; ++j) {
+    const int64_t ej = (int64_t)shfl_u64((uint64_t)e, j);
+    if (j < lane && ej == e) valid = false;
+  }
+  const float v = valid ? logits[t * (int64_t)E + e] : -INFINITY;
+  const float vmax = wave_max(valid ? v : -INFINITY);
+  const float ex = valid ? expf(v - vmax) : 0.0f;
+  const float s = wave_sum(ex);
+  if (act) {
+    idx[t * k + lane] = valid ? (int32_t)e : -1;
+    w[t * k + lane] = valid ? ex / s : 0.0f;
+    if (!valid) atomicAdd(status, 1);
+  }
+}
+
+// ------------------------------------------------------------ dispatch plan
+// Tokens are cut into chunks of 64 (one wavefront each).  For every chunk c
+// and expert e the plan keeps the 64-bit set of chunk lanes routed to e; the
+// permuted row of (t, e) is then
+//   seg[e] + sum_{c' < c} popcount(mask[c'][e]) + popcount(mask[c][e] & lanes_below(t))
+// which is exactly the stable expert-major / token-ascending order.
+__global__ __launch_bounds__(256) void plan_count_kernel(
+    const int32_t *__restrict__ idx, int64_t T, int E, int k,
+    uint64_t *__restrict__ masks, int32_t *__restrict__ chunk_cnt,
+    int32_t *__restrict__ status) {
+  extern __shared__ uint64_t lds_mask[];  // [4][E]
+  const int wv = threadIdx.x >> 6, lane = lane_id();
+  const int64_t nchunks = (T + 63) >> 6;
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + wv;
+  uint64_t *m = lds_mask + wv * E;
+  for (int e = lane; e < E; e += kWave) m[e] = 0ull;
+  __syncthreads();
+  const int64_t t = chunk * 64 + lane;
+  if (chunk < nchunks && t < T) {
+    const uint64_t bit = 1ull << lane;
+    for (int j = 0; j < k; ++j) {
+      const int e = idx[t * k + j];
+      if (e < 0 || e >= E) {
+        atomicAdd(status, 1);
+        continue;
+      }
+      const uint64_t old = atomicOr((unsigned long long *)&m[e], (unsigned long long)bit);
+      if (old & bit) atomicAdd(status, 1);
+    }
+  }
+  __syncthreads();
+  if (chunk < nchunks) {
+    for (int e = lane; e < E; e += kWave) {
+      masks[chunk * E + e] = m[e];
+      chunk_cnt[chunk * E + e] = __popcll(m[e]);
+    }
+  }
+}
+
+// Block-wide exclusive scan of one int per thread (blockDim.x <= 1024).
+__device__ int block_exclusive_scan(int v, int *total) {
+  __shared__ int wsum[16];
+  const int lane = lane_id(), wv = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == kWave - 1) wsum[wv] = incl;
+  __syncthreads();
+  int base = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    if (i < wv) base += wsum[i];
+    tot += wsum[i];
+  }
+  *total = tot;
+  return base + incl - v;
+}
+
+// One workgroup per expert: exclusive scan of its per-chunk counts.
+__global__ __launch_bounds__(256) void plan_scan_kernel(
+    const int32_t *__restrict__ chunk_cnt, int64_t nchunks, int E,
+    int32_t *__restrict__ chunk_base, int32_t *__restrict__ counts) {
+  const int e = blockIdx.x;
+  const int64_t per = (nchunks + blockDim.x - 1) / blockDim.x;
+  const int64_t c0 = threadIdx.x * per;
+  const int64_t c1 = c0 + per < nchunks ? c0 + per : nchunks;
+  int s = 0;
+  for (int64_t c = c0; c < c1; ++c) s += chunk_cnt[c * E + e];
+  int total;
+  int run = block_exclusive_scan(s, &total);
+  for (int64_t c = c0; c < c1; ++c) {
+    chunk_base[c * E + e] = run;
+    run += chunk_cnt[c * E + e];
+  }
+  if (threadIdx.x == 0) counts[e] = total;
+}
+
+// Segment table from counts: row offsets plus row-tile prefixes for BM = 32<<b.
+template <typename CT>
+__global__ __launch_bounds__(1024) void segments_kernel(const CT *__restrict__ counts, int E,
+                                                        int32_t *__restrict__ seg) {
+  const int e = threadIdx.x;
+  const int c = e < E ? (int)counts[e] : 0;
+#pragma unroll
+  for (int b = 0; b <= ART_MOE_SEG_NBM; ++b) {
+    int v;
+    if (b == 0) {
+      v = c;
+    } else {
+      const int bm = 32 << (b - 1);
+      v = (c + bm - 1) / bm;
+    }
+    int total;
+    const int ex = block_exclusive_scan(v, &total);
+    if (e < E) seg[b * (E + 1) + e] = ex;
+    if (e == 0) seg[b * (E + 1) + E] = total;
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_scatter_kernel(
+    const int32_t *__restrict__ idx, const float *__restrict__ w, int64_t T, int E, int k,
+    const uint64_t *__restrict__ masks, const int32_t *__restrict__ chunk_base,
+    const int32_t *__restrict__ seg, int32_t *__restrict__ dest,
+    int32_t *__restrict__ row_token, float *__restrict__ row_prob) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * k) return;
+  const int64_t t = i / k;
+  const int j = (int)(i - t * k);
+  const int e = idx[i];
+  bool ok = e >= 0 && e < E;
+  for (int jj = 0; jj < j; ++jj)
+    if (idx[t * k + jj] == e) ok = false;
+  if (!ok) {
+    dest[i] = -1;
+    return;
+  }
+  const int64_t c = t >> 6;
+  const int lane = (int)(t & 63);
+  const uint64_t m = masks[c * E + e];
+  const uint64_t below = lane ? (m & ((1ull << lane) - 1ull)) : 0ull;
+  const int pos = seg[e] + chunk_base[c * E + e] + __popcll(below);
+  dest[i] = pos;
+  row_token[pos] = (int32_t)t;
+  if (row_prob) row_prob[pos] = w[i];
+}
+
+// ---------------------------------------------------------- permute / combine
+// One wavefront per token; rows move as 16-byte chunks of 8 bf16.
+__global__ __launch_bounds__(256) void permute_kernel(const U4 *__restrict__ x,
+                                                      const int32_t *__restrict__ dest,
+                                                      int64_t T, int k, int H8,
+                                                      U4 *__restrict__ xp) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int my_dest = lane < k ? dest[t * k + lane] : -1;
+  const U4 *src = x + t * H8;
+  for (int c0 = 0; c0 < H8; c0 += 4 * kWave) {
+    U4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + u * kWave + lane;
+      if (c < H8) v[u] = src[c];
+    }
+    for (int j = 0; j < k; ++j) {
+      const int d = __shfl(my_dest, j, kWave);
+      if (d < 0) continue;
+      U4 *dst = xp + (int64_t)d * H8;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + u * kWave + lane;
+        if (c < H8) dst[c] = v[u];
+      }
+    }
+  }
+}
+
+constexpr int kMaxK = 32;
+
+__global__ __launch_bounds__(256) void combine_kernel(
+    const U4 *__restrict__ yp, const int32_t *__restrict__ dest, const float *__restrict__ wgt,
+    const float *__restrict__ dl, const int32_t *__restrict__ idx, const U4 *__restrict__ w_r,
+    int64_t T, int k, int H8, U4 *__restrict__ y) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const bool act = lane < k;
+  const int my_dest = act ? dest[t * k + lane] : -1;
+  const float my_w = (act && wgt) ? wgt[t * k + lane] : 1.0f;
+  const int my_e = (act && w_r) ? idx[t * k + lane] : -1;
+  const float my_dl = (act && w_r) ? dl[t * k + lane] : 0.0f;
+  for (int c = lane; c < H8; c += kWave) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      const int d = __shfl(my_dest, j, kWave);
+      const float wj = __shfl(my_w, j, kWave);
+      if (d < 0) continue;
+      float f[8];
+      unpack8(yp[(int64_t)d * H8 + c], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += wj * f[i];
+    }
+    if (w_r) {
+      for (int j = 0; j < k; ++j) {
+        const int e = __shfl(my_e, j, kWave);
+        const float lj = __shfl(my_dl, j, kWave);
+        if (e < 0) continue;
+        float f[8];
+        unpack8(w_r[(int64_t)e * H8 + c], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += lj * f[i];
+      }
+    }
+    y[t * H8 + c] = pack8(acc);
+  }
+}
+
+// dl[t,j] = w_j * (dw_j - sum_i w_i dw_i), dw_j = sum_p dp_part[p][dest[t,j]].
+__global__ __launch_bounds__(256) void router_backward_kernel(
+    const float *__restrict__ dp_part, int n_part, int64_t M, const int32_t *__restrict__ dest,
+    const float *__restrict__ w, const int32_t *__restrict__ idx, int64_t T, int E, int k,
+    float *__restrict__ dl, float *__restrict__ dlogits) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const bool act = lane < k;
+  const int d = act ? dest[t * k + lane] : -1;
+  float dw = 0.0f;
+  if (d >= 0)
+    for (int p = 0; p < n_part; ++p) dw += dp_part[(int64_t)p * M + d];
+  const float wj = (act && d >= 0) ? w[t * k + lane] : 0.0f;
+  const float s = wave_sum(wj * dw);
+  const float g = wj * (dw - s);
+  if (act) dl[t * k + lane] = g;
+  if (dlogits) {
+    const int my_e = (act && d >= 0) ? idx[t * k + lane] : -1;
+    int ej[kMaxK];
+    float gj[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
+      ej[j] = __shfl(my_e, j, kWave);
+      gj[j] = __shfl(g, j, kWave);
+    }
+    for (int e = lane; e < E; e += kWave) {
+      float v = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kMaxK; ++j)
+        if (j < k && ej[j] == e) v = gj[j];
+      dlogits[t * (int64_t)E + e] = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------ transpose
+__global__ __launch_bounds__(256) void transpose_kernel(const bf16 *__restrict__ src, int R, int C,
+                                                        int64_t s_es, int64_t s_ld,
+                                                        bf16 *__restrict__ dst, int64_t d_es,
+                                                        int64_t d_ld, float scale) {
+  __shared__ float tile[32][33];
+  const int e = blockIdx.z;
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  const bf16 *s = src + e * s_es;
+  bf16 *d = dst + e * d_es;
+  for (int i = ty; i < 32; i += 8) {
+    const int r = r0 + i, c = c0 + tx;
+    tile[i][tx] = (r < R && c < C) ? (float)s[(int64_t)r * s_ld + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int c = c0 + i, r = r0 + tx;
+    if (r < R && c < C) d[(int64_t)c * d_ld + r] = (bf16)(scale * tile[tx][i]);
+  }
+}
+
+}  // namespace art
+
+using namespace art;
+
+// ================================================================ C ABI
+extern "C" int art_moe_router_topk(const float *logits, int64_t T, int32_t E, int32_t k,
+                                   int32_t *idx, float *w, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && E >= 1 && E <= 1024, "router_topk: need T >= 0 and 1 <= E <= 1024 (T=%lld E=%d)", (long long)T, E);
+  ART_REQUIRE(k >= 1 && k <= E && k <= kMaxK, "router_topk: need 1 <= k <= min(E, 32) (k=%d)", k);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(logits && idx && w, "router_topk: null pointer");
+  const dim3 grid((unsigned)((T + 3) / 4));
+  hipStream_t s = as_stream(stream);
+  const int epl = (E + 63) / 64;
+  if (epl <= 1) topk_softmax_kernel<1><<<grid, 256, 0, s>>>(logits, T, E, k, idx, w);
+  else if (epl <= 2) topk_softmax_kernel<2><<<grid, 256, 0, s>>>(logits, T, E, k, idx, w);
+  else if (epl <= 4) topk_softmax_kernel<4><<<grid, 256, 0, s>>>(logits, T, E, k, idx, w);
+  else if (epl <= 8) topk_softmax_kernel<8><<<grid, 256, 0, s>>>(logits, T, E, k, idx, w);
+  else topk_softmax_kernel<16><<<grid, 256, 0, s>>>(logits, T, E, k, idx, w);
+  return check_launch("router_topk");
+}
+
+extern "C" int art_moe_router_replay(const float *logits, const int64_t *target, int64_t T,
+                                     int32_t E, int32_t k, int32_t *idx, float *w,
+                                     int32_t *status, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && E >= 1, "router_replay: need T >= 0 and E >= 1");
+  ART_REQUIRE(k >= 1 && k <= E && k <= kMaxK, "router_replay: need 1 <= k <= min(E, 32) (k=%d)", k);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(logits && target && idx && w && status, "router_replay: null pointer");
+  replay_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(logits, target, T, E, k,
+                                                                             idx, w, status);
+  return check_launch("router_replay");
+}
+
+extern "C" int art_moe_router_backward(const float *dp_part, int32_t n_part, int64_t M,
+                                       const int32_t *dest, const float *w, const int32_t *idx,
+                                       int64_t T, int32_t E, int32_t k, float *dl, float *dlogits,
+                                       void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && E >= 1 && k >= 1 && k <= kMaxK && n_part >= 0,
+              "router_backward: bad sizes (T=%lld E=%d k=%d n_part=%d)", (long long)T, E, k, n_part);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(dest && w && dl && (n_part == 0 || dp_part) && (!dlogits || idx),
+              "router_backward: null pointer");
+  router_backward_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      dp_part, n_part, M, dest, w, idx, T, E, k, dl, dlogits);
+  return check_launch("router_backward");
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+extern "C" size_t art_moe_plan_workspace_bytes(int64_t T, int32_t E) {
+  if (T < 0 || E < 1) return 0;
+  const size_t nch = (size_t)((T + 63) / 64);
+  return align256(nch * E * sizeof(uint64_t)) + 2 * align256(nch * E * sizeof(int32_t));
+}
+
+extern "C" int art_moe_dispatch_plan(const int32_t *idx, const float *w, int64_t T, int32_t E,
+                                     int32_t k, int32_t *counts, int32_t *seg, int32_t *dest,
+                                     int32_t *row_token, float *row_prob, int32_t *status,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && E >= 1 && E <= 1024, "dispatch_plan: need 1 <= E <= 1024 (E=%d)", E);
+  ART_REQUIRE(k >= 1 && k <= E && k <= kMaxK, "dispatch_plan: need 1 <= k <= min(E, 32) (k=%d)", k);
+  ART_REQUIRE(T * (int64_t)k < (int64_t)INT32_MAX, "dispatch_plan: T*k must fit int32");
+  ART_REQUIRE(counts && seg && status, "dispatch_plan: null pointer");
+  const size_t need = art_moe_plan_workspace_bytes(T, E);
+  ART_REQUIRE(workspace_bytes >= need, "dispatch_plan: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const int64_t nch = (T + 63) / 64;
+  char *ws = (char *)workspace;
+  uint64_t *masks = (uint64_t *)ws;
+  int32_t *ccnt = (int32_t *)(ws + align256(nch * E * sizeof(uint64_t)));
+  int32_t *cbase = (int32_t *)((char *)ccnt + align256(nch * E * sizeof(int32_t)));
+  if (T > 0) {
+    ART_REQUIRE(idx && dest && row_token && (!row_prob || w), "dispatch_plan: null pointer");
+    plan_count_kernel<<<dim3((unsigned)((nch + 3) / 4)), 256, 4 * E * sizeof(uint64_t), s>>>(
+        idx, T, E, k, masks, ccnt, status);
+    int rc = check_launch("dispatch_plan/count");
+    if (rc) return rc;
+    plan_scan_kernel<<<dim3(E), 256, 0, s>>>(ccnt, nch, E, cbase, counts);
+    rc = check_launch("dispatch_plan/scan");
+    if (rc) return rc;
+    segments_kernel<int32_t><<<1, 1024, 0, s>>>(counts, E, seg);
+    rc = check_launch("dispatch_plan/segments");
+    if (rc) return rc;
+    const int64_t n = T * k;
+    plan_scatter_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, s>>>(
+        idx, w, T, E, k, masks, cbase, seg, dest, row_token, row_prob);
+    return check_launch("dispatch_plan/scatter");
+  }
+  // T == 0: all experts empty.
+  plan_scan_kernel<<<dim3(E), 256, 0, s>>>(ccnt, 0, E, cbase, counts);
+  int rc = check_launch("dispatch_plan/scan");
+  if (rc) return rc;
+  segments_kernel<int32_t><<<1, 1024, 0, s>>>(counts, E, seg);
+  return check_launch("dispatch_plan/segments");
+}
+
+extern "C" int art_moe_segments_from_counts(const int64_t *counts, int32_t E, int32_t *seg,
+                                            void *stream) {
+  clear_error();
+  ART_REQUIRE(E >= 1 && E <= 1024, "segments_from_counts: need 1 <= E <= 1024 (E=%d)", E);
+  ART_REQUIRE(counts && seg, "segments_from_counts: null pointer");
+  segments_kernel<int64_t><<<1, 1024, 0, as_stream(stream)>>>(counts, E, seg);
+  return check_launch("segments_from_counts");
+}
+
+extern "C" int art_moe_permute(const void *x, const int32_t *dest, int64_t T, int32_t k,
+                               int32_t H, void *x_perm, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0,
+              "permute: need H %% 8 == 0 and 1 <= k <= 32 (H=%d k=%d)", H, k);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(x && dest && x_perm, "permute: null pointer");
+  permute_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      (const U4 *)x, dest, T, k, H / 8, (U4 *)x_perm);
+  return check_launch("permute");
+}
+
+extern "C" int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
+                               const float *dl, const int32_t *idx, const void *w_r, int64_t T,
+                               int32_t k, int32_t H, void *y, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0,
+              "combine: need H %% 8 == 0 and 1 <= k <= 32 (H=%d k=%d)", H, k);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(y_perm && dest && y && (!w_r || (dl && idx)), "combine: null pointer");
+  combine_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      (const U4 *)y_perm, dest, wgt, dl, idx, (const U4 *)w_r, T, k, H / 8, (U4 *)y);
+  return check_launch("combine");
+}
+
+extern "C" int art_moe_transpose(const void *src, int32_t E, int32_t R, int32_t C, int64_t s_es,
+                                 int64_t s_ld, void *dst, int64_t d_es, int64_t d_ld, float scale,
+                                 void *stream) {
+  clear_error();
+  ART_REQUIRE(E >= 0 && R >= 0 && C >= 0, "transpose: negative size");
+  if (E == 0 || R == 0 || C == 0) return ART_MOE_OK;
+  ART_REQUIRE(src && dst, "transpose: null pointer");
+  ART_REQUIRE(E <= 65535, "transpose: E too large");
+  const dim3 grid((unsigned)((C + 31) / 32), (unsigned)((R + 31) / 32), (unsigned)E);
+  transpose_kernel<<<grid, 256, 0, as_stream(stream)>>>((const bf16 *)src, R, C, s_es, s_ld,
+                                                        (bf16 *)dst, d_es, d_ld, scale);
+  return check_launch("transpose");
+}

@@ -1,0 +1,225 @@
+"""Benchmark: MoE-LoRA expert layer forward + backward on one MI355X.
+
+One step = the layer forward (router gating linear, top-k softmax, dispatch
+plan, FC1 + LoRA + weighted SwiGLU, FC2 + LoRA, combine) and its backward (dx
+including the router path, and the six LoRA weight gradients) over one batch of
+T synthetic tokens already resident in HBM.  Base weights are frozen.
+
+Prints one JSON line (the driver's contract) with:
+  value       tokens / second (whole job, one GPU)
+  roofline    the dominant kernel (FC1 + LoRA + SwiGLU forward) timed with HIP
+              events on the stream it is launched on, against bf16 MFMA peak
+  kernels     per-op average ms per step (HIP events), with roofline fractions
+  cpu_baseline  the CPU oracle (torch fp32 restatement of the reference path)
+              timed on the host cores over a bounded token sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from collections import defaultdict
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "art-mlx_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "MoE-LoRA layer tokens/sec fwd+bwd (Qwen3-30B-A3B shape, 1 GPU); % MFMA/HBM peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
+
+# ops whose time counts as GEMM (MFMA roofline) vs bandwidth-bound (HBM roofline)
+GEMM_OPS = ("grouped_gemm", "fc1_swiglu", "fc2_dgrad_swiglu", "grouped_wgrad")
+HBM_OPS = ("router_topk", "router_replay", "dispatch_plan", "combine", "router_backward",
+           "permute", "transpose_into", "segments_from_counts")
+
+
+class OpTimer:
+    """Brackets every art_amd.ops call with HIP events on torch's current stream
+    (the stream every op launches on) and accumulates per-op durations."""
+
+    def __init__(self, ops_module):
+        import torch
+        self.torch = torch
+        self.ops = ops_module
+        self.enabled = False
+        self.pending = []
+        self.orig = {}
+        for name in GEMM_OPS + HBM_OPS:
+            fn = getattr(ops_module, name)
+            self.orig[name] = fn
+            setattr(ops_module, name, self._wrap(name, fn))
+
+    def _wrap(self, name, fn):
+        torch = self.torch
+
+        def wrapped(*a, **kw):
+            if not self.enabled:
+                return fn(*a, **kw)
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            out = fn(*a, **kw)
+            e.record()
+            self.pending.append((name, s, e))
+            return out
+        return wrapped
+
+    def collect(self):
+        tot = defaultdict(float)
+        cnt = defaultdict(int)
+        for name, s, e in self.pending:
+            tot[name] += s.elapsed_time(e)
+            cnt[name] += 1
+        return tot, cnt
+
+
+def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0):
+    import torch
+
+    from art_amd import ops
+    from art_amd.megatron import moe_layer
+    from art_amd.workloads import make_inputs
+
+    dev = torch.device("cuda:0")
+    inp = make_inputs(cfg, dev, seed=seed)
+    base = moe_layer.FrozenExperts.build(inp.w_r, inp.w1, inp.w2)
+    lora = {n: inp.lora[n].requires_grad_() for n in NAMES}
+    x = inp.x.requires_grad_()
+    s = cfg.scale
+    logits = inp.logits if cfg.replay else None
+    target = inp.target if cfg.replay else None
+    dy = inp.dy
+    timer = OpTimer(ops)
+
+    def step():
+        x.grad = None
+        for v in lora.values():
+            v.grad = None
+        y, _idx, _counts, _status = moe_layer.moe_lora_layer(
+            x, base, *(lora[n] for n in NAMES), k=cfg.k, scales=(s, s, s), logits=logits,
+            target=target)
+        y.backward(dy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    timer.enabled = False
+    tot, cnt = timer.collect()
+    return (t1 - t0) * 1e3 / steps, tot, cnt
+
+
+def cpu_baseline(cfg, tokens: int, iters: int, seed: int = 0):
+    """The CPU oracle (torch fp32 restatement of the reference path) on ``tokens`` tokens."""
+    import torch
+
+    from art_amd.workloads import make_inputs
+    from oracle import layer as OL
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    inp = make_inputs(cfg, "cpu", seed=seed, T=tokens, dtype=torch.float32)
+    leaves = {n: inp.lora[n].requires_grad_() for n in NAMES}
+    s = cfg.scale
+    p = OL.LayerParams(w_r=None if cfg.replay else inp.w_r, w1=inp.w1, w2=inp.w2,
+                       scale_g=s, scale_u=s, scale_d=s, **leaves)
+
+    def step():
+        x = inp.x.clone().requires_grad_()
+        for v in leaves.values():
+            v.grad = None
+        y, _ = OL.moe_lora_layer(x, p, cfg.k, logits=inp.logits, target=inp.target)
+        y.backward(inp.dy)
+
+    step()  # warmup
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        step()
+    dt = (time.perf_counter() - t0) / iters
+    return {"value": round(tokens / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"{tokens} tokens of {cfg.name} (all {cfg.E} experts, full widths), fp32 "
+                       f"weights, fwd+bwd, {iters} timed iters after 1 warmup; "
+                       f"{dt:.2f} s/iter on {threads} threads")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C1")
+    ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--cpu-iters", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the expert-parallel sharding design is described in DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from art_amd.workloads import CONFIGS
+    cfg = CONFIGS[args.config]
+    ms, tot, cnt = gpu_bench(cfg, args.steps, args.warmup)
+    flops = cfg.flops_fwd_bwd()
+    tokens_per_s = cfg.T / (ms / 1e3)
+
+    # dominant kernel: FC1 + LoRA K-extension + SwiGLU forward (one launch per step)
+    m, h, f, r = cfg.M, cfg.H, cfg.F, cfg.r
+    fc1_flops = 2 * m * h * 2 * f + 2 * m * 2 * f * r
+    fc1_ms = tot["fc1_swiglu"] / max(cnt["fc1_swiglu"], 1)
+    fc1_tflops = fc1_flops / (fc1_ms * 1e-3) / 1e12
+    gemm_ms = sum(tot[n] for n in GEMM_OPS) / args.steps
+    hbm_ms = sum(tot[n] for n in HBM_OPS) / args.steps
+    gemm_flops = flops["base"] + flops["lora"] + flops["router"]
+    comb_ms = tot["combine"] / args.steps
+    # combine fwd reads M rows, writes T rows; the dx un-permute also reads k router rows (L2)
+    comb_bytes = 2 * (cfg.M * h * 2 + cfg.T * h * 2) + 2 * cfg.M * 4
+    kernels = {name: round(tot[name] / args.steps, 4) for name in sorted(tot)}
+
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded: x~N(0,1), W_r~N(0,1/H), frozen base W~N(0,0.02), LoRA A,B~N(0,0.01))",
+        "config": {"workload": f"{cfg.name}: {cfg.note}, layer fwd+bwd", "T": cfg.T, "H": h,
+                   "E": cfg.E, "k": cfg.k, "F": f, "r": r, "alpha": cfg.alpha,
+                   "routing": "replay Zipf(1.2)" if cfg.replay else "top-k softmax (renormalised)",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd)",
+                     "achieved": round(fc1_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(fc1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": fc1_flops, "avg_launch_ms": round(fc1_ms, 4)},
+        "gemm_mfma_frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "gemm_ms_per_step": round(gemm_ms, 4),
+        "bandwidth_ops_ms_per_step": round(hbm_ms, 4),
+        "combine_hbm_frac": round(comb_bytes / (comb_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if comb_ms else None,
+        "kernels_ms_per_step": kernels,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens, args.cpu_iters)
+        result["cpu_baseline"]["gpu_over_cpu"] = round(tokens_per_s / result["cpu_baseline"]["value"], 1)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,220 @@
+/*
+ * art_moe.h -- C ABI of the MI355X (gfx950) MoE-LoRA expert-layer library
+ * (libart_moe.so, built from art-mlx_amd/csrc/).
+ *
+ * The library replaces, for one GPU, the device work behind these reference
+ * entry points (paths under the reference tree):
+ *   - megatron TopKRouter.routing / RouterReplay.get_replay_topk, as used by
+ *     src/art/megatron/routing_replay.py:1388-1435 and restated in
+ *     src/art/megatron/dsv4/layer.py:139-191;
+ *   - megatron moe_utils.permute / unpermute (fused TE mask-map kernels,
+ *     src/art/megatron/provider.py:604; signature
+ *     src/art/megatron/runtime/bridge_runtime.py:870-879);
+ *   - TE GroupedLinear base products called from MLPExpertsLinearFC1LoRA /
+ *     MLPExpertsLinearFC2LoRA (src/art/megatron/lora.py:1512-1529, 1556-1571);
+ *   - the QuACK varlen-M / varlen-K grouped LoRA GEMMs of
+ *     src/art/megatron/kernels/cute_grouped_lora_quack.py:257-438, 441-629;
+ *   - megatron weighted_bias_swiglu_impl / weighted_swiglu_back
+ *     (src/art/megatron/compile_workarounds.py:73-106).
+ *
+ * Conventions
+ *   - Every buffer is caller-owned device memory (allocate with hipMalloc or a
+ *     framework allocator); the library allocates nothing.
+ *   - bf16 buffers are passed as void* holding IEEE bfloat16 (uint16 bits).
+ *   - `stream` is a hipStream_t passed as void* (NULL = legacy stream).  All
+ *     work of one call is enqueued on that stream; calls do not synchronize.
+ *   - Return value: ART_MOE_OK (0) or a negative ART_MOE_ERR_* code; a
+ *     message for the last error of the calling thread is available from
+ *     art_moe_last_error().  No C++ exception crosses this boundary.
+ *   - Value checks that would need a device->host copy (expert ids in range,
+ *     no repeated id in a row) are reported through a caller-zeroed device
+ *     int32 `status` counter instead of the return code.
+ *
+ * Segment table ("seg"): int32 array of ART_MOE_SEG_LEN(E) entries on the
+ *   device.  seg[0 .. E] are the row offsets of the E expert segments
+ *   (exclusive prefix of tokens_per_expert); seg[(1+b)*(E+1) + e] for
+ *   b = 0..ART_MOE_SEG_NBM-1 is the exclusive prefix over experts of
+ *   ceil(count_e / BM_b) with BM_b = 32 << b (row-tile schedule of the grouped
+ *   GEMMs).  Build it with art_moe_dispatch_plan or art_moe_segments_from_counts.
+ */
+#ifndef ART_MOE_H
+#define ART_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ART_MOE_OK 0
+#define ART_MOE_ERR_INVALID_ARG (-1)
+#define ART_MOE_ERR_UNSUPPORTED (-2)
+#define ART_MOE_ERR_HIP (-3)
+
+#define ART_MOE_SEG_NBM 4
+#define ART_MOE_SEG_LEN(E) ((1 + ART_MOE_SEG_NBM) * ((E) + 1))
+
+/* Library version, e.g. 100 for 0.1.0. */
+int art_moe_version(void);
+
+/* Message of the last error returned on this thread ("" if none). */
+const char *art_moe_last_error(void);
+
+/* ---------------------------------------------------------------- routing */
+
+/* Top-k softmax routing over fp32 logits [T,E] (row-major).
+ * idx[T,k] receives the k selected expert ids in descending logit order (tie:
+ * lower id first; NaN above every number), w[T,k] the softmax of the k
+ * selected logits (fp32).  E <= 1024, 1 <= k <= min(E, 32).
+ * Replaces: megatron TopKRouter.routing with score_function="softmax",
+ * pre_softmax=False (contract: tests/unit/test_moe_routing_replay.py:181-205). */
+int art_moe_router_topk(const float *logits, int64_t T, int32_t E, int32_t k,
+                        int32_t *idx, float *w, void *stream);
+
+/* Routing replay: target[T,k] (int64) replaces the top-k selection, w = softmax
+ * of the gathered logits.  Ids outside [0,E) or repeated within a row add 1
+ * to *status each and get weight 0 and id -1.
+ * Replaces: RouterReplay.get_replay_topk fed by
+ * MoeRoutingReplayController._prepare_native_target_for_router
+ * (src/art/megatron/routing_replay.py:1388-1435). */
+int art_moe_router_replay(const float *logits, const int64_t *target, int64_t T,
+                          int32_t E, int32_t k, int32_t *idx, float *w,
+                          int32_t *status, void *stream);
+
+/* Router backward through the renormalised softmax.  dp_part holds n_part
+ * fp32 partial vectors of length M (stride M) whose sum is dL/dp per permuted
+ * row; dl[T,k] = w * (dw - sum_j w_j dw_j) with dw[t,j] = dp[dest[t,j]].
+ * If dlogits != NULL it receives the dense [T,E] gradient (zeros outside the
+ * selected ids).  Replaces the autograd of the routing softmax/gather. */
+int art_moe_router_backward(const float *dp_part, int32_t n_part, int64_t M,
+                            const int32_t *dest, const float *w,
+                            const int32_t *idx, int64_t T, int32_t E, int32_t k,
+                            float *dl, float *dlogits, void *stream);
+
+/* ---------------------------------------------------------- dispatch plan */
+
+/* Bytes of scratch art_moe_dispatch_plan needs for T tokens and E experts. */
+size_t art_moe_plan_workspace_bytes(int64_t T, int32_t E);
+
+/* Expert-major, token-ascending dispatch plan from idx[T,k].
+ * Outputs: counts[E] (tokens per expert, int32), seg[ART_MOE_SEG_LEN(E)],
+ * dest[T,k] (permuted row of token t's j-th expert, -1 for rejected ids),
+ * row_token[M] (token of each permuted row, M = T*k), and, if w != NULL,
+ * row_prob[M] = w[t,j] of the row.  Out-of-range or repeated ids add to
+ * *status (caller-zeroed) and are dropped (rows of the segment table then
+ * sum to less than M).
+ * Replaces: moe_utils.permute's sorted_indices / tokens_per_expert
+ * (routing_map.sum(0)) with moe_permute_fusion=True (provider.py:604). */
+int art_moe_dispatch_plan(const int32_t *idx, const float *w, int64_t T,
+                          int32_t E, int32_t k, int32_t *counts, int32_t *seg,
+                          int32_t *dest, int32_t *row_token, float *row_prob,
+                          int32_t *status, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+/* Segment table from per-expert counts (int64 device array [E]).
+ * Replaces: _build_expert_offsets (cute_grouped_lora_quack.py:109-121),
+ * without its host round trip. */
+int art_moe_segments_from_counts(const int64_t *counts, int32_t E, int32_t *seg,
+                                 void *stream);
+
+/* -------------------------------------------------------- permute/combine */
+
+/* x_perm[dest[t,j], :] = x[t, :] for bf16 rows of H (H % 8 == 0).
+ * Replaces: moe_utils.permute (tokens gather). */
+int art_moe_permute(const void *x, const int32_t *dest, int64_t T, int32_t k,
+                    int32_t H, void *x_perm, void *stream);
+
+/* y[t, :] = sum_j (wgt ? wgt[t,j] : 1) * y_perm[dest[t,j], :]
+ *           + (w_r ? sum_j dl[t,j] * w_r[idx[t,j], :] : 0)
+ * fp32 accumulation in slot order j = 0..k-1, bf16 out.  With w_r == NULL
+ * this is moe_utils.unpermute (combine); with w_r it also adds the router
+ * input gradient dl @ W_r restricted to the k selected experts. */
+int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
+                    const float *dl, const int32_t *idx, const void *w_r,
+                    int64_t T, int32_t k, int32_t H, void *y, void *stream);
+
+/* ------------------------------------------------------------- grouped GEMM */
+
+/* Grouped "NT" product over expert segments of seg:
+ *   C[m, n] = alpha * ( sum_c A[row(m), c] * B[e][n, c]
+ *                     + sum_j Tl[m, j] * L[e][n, j] )       m in segment e
+ * A bf16 rows of K (lda), row(m) = a_rows ? a_rows[m] : m; B bf16 [E][N][K]
+ * (ldb, b_estride); optional LoRA K-extension Tl bf16 [M][kt] (ldt) and
+ * L bf16 [E][N][kt] (ldl, l_estride), kt % 16 == 0 (kt = 0: none).
+ * C is bf16 (c_fp32 = 0) or fp32 (c_fp32 = 1) with leading dimension ldc.
+ * K % 8 == 0.  Rows of C outside every segment are not written.
+ * Replaces: TE GroupedLinear forward/dgrad (lora.py:1515-1521, 1559-1565),
+ * QuACK varlen-M GEMMs (cute_grouped_lora_quack.py:257-298) and the
+ * base + adapter add (lora.py:1529, 1571). */
+int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
+                         const void *b, int64_t ldb, int64_t b_estride,
+                         const void *tl, int64_t ldt, const void *l,
+                         int64_t ldl, int64_t l_estride, int32_t kt,
+                         const int32_t *seg, int32_t E, int64_t M, int32_t N,
+                         int32_t K, float alpha, void *c, int64_t ldc,
+                         int32_t c_fp32, void *stream);
+
+/* FC1 with the weighted SwiGLU fused into the epilogue.
+ * y1 = A @ W1[e]^T + Tl @ L1[e]^T with W1 [E][2F][K], L1 [E][2F][kt];
+ * writes y1 (bf16 [M][2F], gate columns first) and
+ * h[m, f] = silu(g) * u * row_prob[m] (bf16 [M][F]) where g = y1[m, f],
+ * u = y1[m, F + f] rounded to bf16 first.  F % 64 == 0.
+ * Replaces: MLPExpertsLinearFC1LoRA.forward (lora.py:1512-1529) followed by
+ * weighted_bias_swiglu_impl (compile_workarounds.py:73-106). */
+int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
+                       const void *w1, const void *tl, int64_t ldt,
+                       const void *l1, int32_t kt, const int32_t *seg,
+                       int32_t E, int64_t M, int32_t F, int32_t K,
+                       const float *row_prob, void *y1, void *h, void *stream);
+
+/* Number of fp32 partial vectors art_moe_fc2_dgrad_swiglu writes to dp_part. */
+int art_moe_dgrad_swiglu_parts(int32_t F);
+
+/* FC2 data-gradient with the weighted-SwiGLU backward fused into the epilogue.
+ * dh = A @ W2T[e]^T + Tl @ L2[e]^T (W2T [E][F][K]: the FC2 weight transposed;
+ * L2 [E][F][kt]: the down LoRA A_T); with g, u from y1 (bf16 [M][2F]) and
+ * p = row_prob[m]:
+ *   dy1[m, f]     = dh * p * u * sig(g) * (1 + g * (1 - sig(g)))
+ *   dy1[m, F + f] = dh * p * silu(g)
+ *   dp_part[i][m] = partial sums over f of dh * silu(g) * u
+ *                   (i < art_moe_dgrad_swiglu_parts(F)).
+ * Replaces: TE GroupedLinear dgrad of FC2 + QuACK LoRA dgrad
+ * (cute_grouped_lora_quack.py:394-410) + weighted_swiglu_back. */
+int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
+                             const void *w2t, const void *tl, int64_t ldt,
+                             const void *l2, int32_t kt, const int32_t *seg,
+                             int32_t E, int64_t M, int32_t F, int32_t K,
+                             const void *y1, const float *row_prob, void *dy1,
+                             float *dp_part, void *stream);
+
+/* Segmented "TN" product (LoRA weight gradients, fp32 accumulation):
+ *   out[e*o_es + p*o_ps + q*o_qs] (+)=
+ *       alpha * sum_{m in segment e} Lm[lrow(m), p] * R[rrow(m), q]
+ * Lm bf16 rows (ldl) with lrow(m) = l_rows ? l_rows[m] : m, likewise R;
+ * P, Q, ldl, ldr multiples of 8, operands 16-byte aligned.
+ * out is fp32; (o_ps, o_qs) = (Q, 1) writes [E][P][Q], (1, P) writes the
+ * transpose [E][Q][P].  accumulate != 0 adds to out.
+ * Experts with no rows get zeros (or keep out when accumulating).
+ * Replaces: QuACK varlen-K GEMMs for grad_A / grad_B
+ * (cute_grouped_lora_quack.py:301-334, 411-431, 585-616). */
+int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
+                          const void *r, int64_t ldr, const int32_t *r_rows,
+                          const int32_t *seg, int32_t E, int32_t P, int32_t Q,
+                          float alpha, float *out, int64_t o_es,
+                          int64_t o_ps, int64_t o_qs, int32_t accumulate,
+                          void *stream);
+
+/* Batched strided transpose with scale:
+ *   dst[e*d_es + c*d_ld + r] = bf16(scale * src[e*s_es + r*s_ld + c])
+ * for e < E, r < R, c < C (bf16).  Builds transposed frozen-weight copies and
+ * the padded LoRA operand layouts. */
+int art_moe_transpose(const void *src, int32_t E, int32_t R, int32_t C,
+                      int64_t s_es, int64_t s_ld, void *dst, int64_t d_es,
+                      int64_t d_ld, float scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ART_MOE_H */

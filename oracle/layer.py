@@ -1,0 +1,187 @@
+"""torch-CPU restatement of the MoE-LoRA expert layer.  TEST INFRASTRUCTURE ONLY.
+
+Every function computes in ``dtype`` (float32 or float64) on the CPU and is
+differentiated by torch autograd; the backward pass of the layer is therefore
+autograd of this forward.
+
+Reference functions restated (file:line under /root/reference):
+* ``router_logits``     megatron ``router_gating_linear`` with fp32 router:
+                        src/art/megatron/runtime/bridge_runtime.py:775-798,
+                        src/art/megatron/provider.py:605.
+* ``routing``           TopKRouter.routing contract,
+                        tests/unit/test_moe_routing_replay.py:181-205;
+                        src/art/megatron/dsv4/layer.py:139-191 (gather/scatter).
+* ``grouped_linear``    TE GroupedLinear per-expert ``x_e @ weight{e}.T``,
+                        src/art/megatron/lora.py:1097-1100, 1512-1529, 1556-1571.
+* ``grouped_lora``      fp32 per-expert loop, tests/integration/megatron/
+                        model_support/oracle_worker.py:1079-1160; operator
+                        semantics src/art/megatron/kernels/
+                        cute_grouped_lora_quack.py:337-438 (out = s*(x@A)@B).
+* ``grouped_lora_dual`` cute_grouped_lora_quack.py:441-629 / lora.py:1049-1081
+                        (gate columns first, then up).
+* ``weighted_swiglu``   src/art/megatron/compile_workarounds.py:73-106
+                        (``silu(x_glu) * x_linear * weights``, chunk order gate|up).
+* ``permute`` / ``unpermute``  megatron moe_utils permute/unpermute
+                        (signature src/art/megatron/runtime/bridge_runtime.py:870-879):
+                        gather rows expert-major; scatter-add them back.
+* ``moe_lora_layer``    composition as in MLPExpertsLinearFC1LoRA /
+                        MLPExpertsLinearFC2LoRA (lora.py:1512-1529, 1556-1571).
+
+Pinning (tests/test_oracle_layer.py):
+* grads of every function: float64 central finite differences.
+* grouped_lora / grouped_linear: dense equivalence when all experts share one
+  weight (no segmentation involved) and the zero-token-expert KAT shape of
+  tests/integration/test_lora_quack_cutover.py:69-125 (counts [32,0,16,24]).
+* layer wiring (permute, combine, weighting): with identical experts the layer
+  output equals one dense SwiGLU MLP applied to every token, because the k
+  renormalised weights of a token sum to one.
+* weighted_swiglu: finite differences and the closed form at g = 0.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import routing as _routing
+
+
+def router_logits(x: torch.Tensor, w_r: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
+    """logits = x.to(fp32) @ W_r.to(fp32).T  ([T,H] x [E,H] -> [T,E])."""
+    return x.to(dtype) @ w_r.to(dtype).t()
+
+
+def routing(logits: torch.Tensor, k: int, target: torch.Tensor | None = None):
+    """Top-k softmax routing (or replay of ``target``).
+
+    Returns (probs [T,E], routing_map [T,E] bool, idx [T,k] int64, w [T,k]).
+    ``w`` / ``probs`` stay in the autograd graph of ``logits``.
+    """
+    lg = logits.detach().to(torch.float32).numpy()
+    if target is None:
+        idx_np = _routing.topk_indices(lg, k)
+    else:
+        idx_np, _ = _routing.replay(lg, target.cpu().numpy())
+    idx = torch.from_numpy(idx_np.astype(np.int64))
+    sel = logits.gather(1, idx)
+    w = torch.softmax(sel, dim=-1)
+    probs = torch.zeros_like(logits).scatter(1, idx, w)
+    rmap = torch.zeros(logits.shape, dtype=torch.bool).scatter(1, idx, True)
+    return probs, rmap, idx, w
+
+
+def grouped_linear(x: torch.Tensor, weight: torch.Tensor, counts) -> torch.Tensor:
+    """Per-expert ``x_e @ weight[e].T`` over contiguous segments (weight [E,out,in])."""
+    counts = [int(c) for c in counts]
+    outs = []
+    cursor = 0
+    for e, c in enumerate(counts):
+        if c:
+            outs.append(x[cursor:cursor + c] @ weight[e].to(x.dtype).t())
+        cursor += c
+    if cursor != x.shape[0]:
+        raise RuntimeError(f"grouped split mismatch: {cursor} rows vs {x.shape[0]}")
+    if not outs:
+        return x.new_zeros((0, weight.shape[1]))
+    return torch.cat(outs, 0)
+
+
+def grouped_lora(x, a_t, b_t, counts, scale: float) -> torch.Tensor:
+    """Per-expert ``scale * (x_e @ A_T[e]) @ B_T[e]`` (A_T [E,in,r], B_T [E,r,out])."""
+    counts = [int(c) for c in counts]
+    outs = []
+    cursor = 0
+    for e, c in enumerate(counts):
+        if c:
+            xe = x[cursor:cursor + c]
+            outs.append((xe @ a_t[e].to(x.dtype)) @ b_t[e].to(x.dtype))
+        cursor += c
+    if cursor != x.shape[0]:
+        raise RuntimeError(f"grouped split mismatch: {cursor} rows vs {x.shape[0]}")
+    if not outs:
+        return x.new_zeros((0, b_t.shape[-1]))
+    return torch.cat(outs, 0) * scale
+
+
+def grouped_lora_dual(x, gate_a_t, gate_b_t, up_a_t, up_b_t, counts,
+                      scale_gate: float, scale_up: float) -> torch.Tensor:
+    """[gate LoRA | up LoRA] concatenated along the output columns."""
+    return torch.cat(
+        (grouped_lora(x, gate_a_t, gate_b_t, counts, scale_gate),
+         grouped_lora(x, up_a_t, up_b_t, counts, scale_up)), dim=1)
+
+
+def weighted_swiglu(y1: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
+    """``silu(g) * u * w`` with ``g, u = chunk(y1, 2, -1)``; weights [M] or [M,1]."""
+    g, u = torch.chunk(y1, 2, dim=-1)
+    w = weights.reshape(-1, 1).to(y1.dtype)
+    return torch.nn.functional.silu(g) * u * w
+
+
+def permute(x: torch.Tensor, row_token: torch.Tensor) -> torch.Tensor:
+    return x.index_select(0, row_token)
+
+
+def unpermute(y_perm: torch.Tensor, row_token: torch.Tensor, num_tokens: int) -> torch.Tensor:
+    out = y_perm.new_zeros((num_tokens, y_perm.shape[1]))
+    return out.index_add(0, row_token, y_perm)
+
+
+@dataclass
+class LayerParams:
+    """Parameters of one MoE-LoRA expert layer (CPU tensors, any float dtype).
+
+    w_r [E,H] router weight (frozen; None when logits are given)
+    w1  [E,2F,H] FC1 base weight, gate rows first (frozen)
+    w2  [E,H,F]  FC2 base weight (frozen)
+    a_g, a_u [E,H,r]; b_g, b_u [E,r,F]   gate/up LoRA (A_T, B_T layout)
+    a_d [E,F,r]; b_d [E,r,H]             down LoRA
+    scale_g, scale_u, scale_d           alpha / rank
+    """
+    w_r: torch.Tensor | None
+    w1: torch.Tensor
+    w2: torch.Tensor
+    a_g: torch.Tensor
+    b_g: torch.Tensor
+    a_u: torch.Tensor
+    b_u: torch.Tensor
+    a_d: torch.Tensor
+    b_d: torch.Tensor
+    scale_g: float
+    scale_u: float
+    scale_d: float
+
+
+def moe_lora_layer(x: torch.Tensor, p: LayerParams, k: int, *,
+                   logits: torch.Tensor | None = None,
+                   target: torch.Tensor | None = None,
+                   dtype=torch.float32):
+    """Full layer forward in ``dtype``.  Returns (y [T,H], aux dict).
+
+    Exactly one of ``p.w_r`` / ``logits`` supplies the router scores.
+    """
+    xw = x.to(dtype)
+    if logits is None:
+        logits = router_logits(xw, p.w_r, dtype)
+    else:
+        logits = logits.to(dtype)
+    num_experts = p.w1.shape[0]
+    probs, rmap, idx, w = routing(logits, k, target)
+    plan = _routing.dispatch_plan(idx.numpy(), num_experts)
+    row_token = torch.from_numpy(plan["row_token"])
+    counts = plan["counts"].tolist()
+    # permuted probs, expert-major (megatron: probs.T.masked_select(routing_map.T))
+    perm_probs = probs.t().masked_select(rmap.t())
+    x_perm = permute(xw, row_token)
+    y1 = grouped_linear(x_perm, p.w1.to(dtype), counts) + grouped_lora_dual(
+        x_perm, p.a_g.to(dtype), p.b_g.to(dtype), p.a_u.to(dtype), p.b_u.to(dtype),
+        counts, p.scale_g, p.scale_u)
+    h = weighted_swiglu(y1, perm_probs)
+    y2 = grouped_linear(h, p.w2.to(dtype), counts) + grouped_lora(
+        h, p.a_d.to(dtype), p.b_d.to(dtype), counts, p.scale_d)
+    y = unpermute(y2, row_token, x.shape[0])
+    aux = {"logits": logits, "probs": probs, "routing_map": rmap, "idx": idx, "w": w,
+           "plan": plan, "x_perm": x_perm, "y1": y1, "h": h, "y2": y2,
+           "perm_probs": perm_probs}
+    return y, aux

@@ -1,0 +1,140 @@
+"""numpy restatement of the integer routing work.  TEST INFRASTRUCTURE ONLY.
+
+Reference semantics followed
+----------------------------
+* Top-k softmax routing (megatron-core ``TopKRouter.routing`` with the softmax
+  score function and ``moe_router_pre_softmax=False``): top-k over the fp32
+  logits, then softmax over the k selected logits.  That is Qwen3's
+  ``norm_topk_prob`` (softmax over all -> top-k -> renormalise) up to
+  rounding.  Contract: /root/reference/tests/unit/test_moe_routing_replay.py:181-205;
+  restated gather/scatter: /root/reference/src/art/megatron/dsv4/layer.py:139-191;
+  fp32 router: /root/reference/src/art/megatron/provider.py:605.
+* Routing replay (megatron ``RouterReplay.get_replay_topk``): the given target
+  indices replace the top-k; ``selected = scores.gather(1, target)``.
+  Fake: /root/reference/tests/unit/test_moe_routing_replay.py:149-161.
+* Dispatch order (megatron ``moe_utils.permute`` with a routing map, fused TE
+  mask-map kernel, /root/reference/src/art/megatron/provider.py:604): rows are
+  expert-major and token-ascending; ``tokens_per_expert = routing_map.sum(0)``.
+  Canonical order enforced by the reference's own trace tooling:
+  /root/reference/tests/integration/megatron/routing_replay/trace.py:181-232.
+
+Tie rule (a rule of this build; torch's own tie order is unspecified and
+differs between its CPU and CUDA kernels): candidates are ordered by
+descending value, NaN above every number, -0.0 equal to +0.0, and among equal
+values the lower expert index first.
+
+Pinning
+-------
+* ``topk_indices``: brute force over ``sorted()`` of (value, index) pairs on
+  small inputs, constructed ties, NaN rows (tests/test_oracle_routing.py).
+* ``softmax_selected``: closed form ratios w_i / w_j = exp(l_i - l_j) and
+  sum == 1; scipy.special.softmax on the same selected logits.
+* ``dispatch_plan``: the closed form ``arange(T).expand(E, T)
+  .masked_select(routing_map.T)`` (megatron's own construction), the
+  hand-derived KAT from the reference replay test routes
+  (tests/golden/routing_kats.json) and a pure-Python loop on small inputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def _rank_keys(logits: np.ndarray):
+    """Sort keys for one matrix of logits: (is_nan desc, value desc, index asc)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    nan = np.isnan(logits)
+    val = np.where(nan, 0.0, logits).astype(np.float64)
+    val = np.where(val == 0.0, 0.0, val)  # -0.0 ties +0.0
+    return nan, val
+
+
+def topk_indices(logits: np.ndarray, k: int) -> np.ndarray:
+    """Top-k expert ids per row, descending, under the build's tie rule.
+
+    logits: [T, E] float32.  Returns int32 [T, k].
+    """
+    logits = np.asarray(logits, dtype=np.float32)
+    t, e = logits.shape
+    if not (0 < k <= e):
+        raise ValueError(f"need 0 < k <= E, got k={k} E={e}")
+    nan, val = _rank_keys(logits)
+    idx = np.broadcast_to(np.arange(e), (t, e))
+    # lexsort: last key is the primary key.
+    order = np.lexsort((idx, -val, ~nan), axis=-1)
+    return order[:, :k].astype(np.int32)
+
+
+def softmax_selected(logits: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """Renormalised softmax weights over the selected logits (fp64 math, fp32 out)."""
+    sel = np.take_along_axis(np.asarray(logits, np.float64), idx.astype(np.int64), axis=1)
+    sel = sel - sel.max(axis=1, keepdims=True)
+    ex = np.exp(sel)
+    return (ex / ex.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def topk_softmax(logits: np.ndarray, k: int):
+    """(idx int32 [T,k], weights float32 [T,k]) for top-k renormalised softmax routing."""
+    idx = topk_indices(logits, k)
+    return idx, softmax_selected(logits, idx)
+
+
+def replay(logits: np.ndarray, target: np.ndarray):
+    """Routing replay: the target ids replace the top-k; weights = softmax(gather)."""
+    target = np.asarray(target)
+    e = np.asarray(logits).shape[1]
+    if target.size and (target.min() < 0 or target.max() >= e):
+        raise ValueError("replay target contains ids outside [0, num_experts)")
+    for row in target:
+        if len(set(row.tolist())) != len(row):
+            raise ValueError("replay target row repeats an expert id")
+    idx = target.astype(np.int32)
+    return idx, softmax_selected(logits, idx)
+
+
+def routing_map_from_idx(idx: np.ndarray, num_experts: int) -> np.ndarray:
+    """Dense bool [T, E] routing map (the reference router's second output)."""
+    t = idx.shape[0]
+    rmap = np.zeros((t, num_experts), dtype=bool)
+    rows = np.repeat(np.arange(t), idx.shape[1])
+    rmap[rows, idx.reshape(-1)] = True
+    return rmap
+
+
+def dispatch_plan(idx: np.ndarray, num_experts: int):
+    """Expert-major, token-ascending dispatch plan.
+
+    Returns dict with
+      counts    int64 [E]     tokens per expert
+      offsets   int64 [E+1]   exclusive prefix of counts
+      dest      int64 [T,k]   permuted row of (token t, slot j)
+      row_token int64 [M]     token of each permuted row
+      row_slot  int64 [M]     slot j of each permuted row
+    """
+    idx = np.asarray(idx, dtype=np.int64)
+    t, k = idx.shape
+    flat = idx.reshape(-1)
+    if flat.size and (flat.min() < 0 or flat.max() >= num_experts):
+        raise ValueError("expert ids outside [0, num_experts)")
+    # stable sort of the (token-major) flattened pairs by expert id keeps
+    # tokens ascending inside each expert segment.
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=num_experts).astype(np.int64)
+    offsets = np.zeros(num_experts + 1, dtype=np.int64)
+    np.cumsum(counts, out=offsets[1:])
+    dest = np.empty(t * k, dtype=np.int64)
+    dest[order] = np.arange(t * k)
+    return {
+        "counts": counts,
+        "offsets": offsets,
+        "dest": dest.reshape(t, k),
+        "row_token": (order // k).astype(np.int64),
+        "row_slot": (order % k).astype(np.int64),
+    }
+
+
+def row_token_closed_form(routing_map: np.ndarray) -> np.ndarray:
+    """megatron's own construction of the permuted row -> token map:
+    ``arange(T).expand(E, T).masked_select(routing_map.T)``."""
+    rm_t = np.asarray(routing_map, dtype=bool).T
+    tok = np.broadcast_to(np.arange(rm_t.shape[1]), rm_t.shape)
+    return tok[rm_t].astype(np.int64)

@@ -1,0 +1,191 @@
+"""GPU parity of the grouped MFMA GEMM engine against plain torch fp32 (CPU).
+
+Covers ragged segments with zero-token experts, row gather, the LoRA
+K-extension, fp32 output (router logits), the fused SwiGLU forward and
+backward epilogues, and the segmented TN weight-gradient kernel.
+Tolerances: bf16 outputs 1e-2 norm-relative; fp32 outputs 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from art_amd import ops
+    return ops
+
+
+def rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _counts(e, m_total, seed, zeros=True):
+    rng = np.random.default_rng(seed)
+    p = rng.random(e) ** 3
+    if zeros:
+        p[rng.choice(e, size=max(1, e // 4), replace=False)] = 0
+    p /= p.sum()
+    return np.bincount(rng.choice(e, size=m_total, p=p), minlength=e).tolist()
+
+
+def _ref_grouped(a_rows_f, b, counts, tl=None, l=None, alpha=1.0):
+    out = []
+    cur = 0
+    for e, c in enumerate(counts):
+        blk = a_rows_f[cur:cur + c] @ b[e].float().t()
+        if tl is not None:
+            blk = blk + tl[cur:cur + c].float() @ l[e].float().t()
+        out.append(alpha * blk)
+        cur += c
+    return torch.cat(out, 0)
+
+
+CASES = [
+    # e, m, n, k, gather, kt, fp32
+    (8, 1000, 32, 2048, True, 0, False),
+    (8, 1000, 64, 768, False, 0, False),
+    (16, 3000, 1536, 2048, True, 32, False),
+    (128, 4096, 2048, 768, False, 16, False),
+    (4, 300, 200, 72, True, 16, False),
+    (1, 777, 128, 2048, False, 0, True),
+    (5, 64, 96, 64, False, 64, True),
+]
+
+
+@pytest.mark.parametrize("e,m,n,k,gather,kt,fp32", CASES)
+def test_grouped_gemm(device, e, m, n, k, gather, kt, fp32):
+    ops = _ops()
+    print(f"grouped_gemm e={e} m={m} n={n} k={k} gather={gather} kt={kt} fp32={fp32}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    counts = _counts(e, m, seed=m) if e > 1 else [m]
+    t_src = 513
+    src = torch.randn(t_src if gather else m, k, generator=g).to(torch.bfloat16)
+    rows = torch.randint(0, t_src, (m,), generator=g, dtype=torch.int32) if gather else None
+    b = (torch.randn(e, n, k, generator=g) * 0.05).to(torch.bfloat16)
+    tl = l = None
+    if kt:
+        tl = torch.randn(m, kt, generator=g).to(torch.bfloat16)
+        l = (torch.randn(e, n, kt, generator=g) * 0.1).to(torch.bfloat16)
+    seg = ops.segments_from_counts(counts, e, device)
+    got = ops.grouped_gemm(src.to(device), b.to(device), seg, e, m=m,
+                           a_rows=rows.to(device) if gather else None,
+                           tl=tl.to(device) if kt else None, l=l.to(device) if kt else None,
+                           alpha=0.5, out_fp32=fp32)
+    torch.cuda.synchronize()
+    a_f = (src[rows.long()] if gather else src).float()
+    ref = _ref_grouped(a_f, b, counts, tl, l, alpha=0.5)
+    tol = 1e-5 if fp32 else 1e-2
+    assert rel(got, ref) < tol, rel(got, ref)
+    if not fp32:
+        torch.testing.assert_close(got.cpu().float(), ref, atol=3e-2, rtol=3e-2)
+
+
+def test_grouped_gemm_strided_output_and_operand(device):
+    ops = _ops()
+    e, m, k = 3, 200, 64
+    counts = [100, 0, 100]
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(m, 3 * k, generator=g).to(torch.bfloat16)
+    b = torch.randn(e, 48, k, generator=g).to(torch.bfloat16)
+    seg = ops.segments_from_counts(counts, e, device)
+    out = torch.zeros(m, 100, dtype=torch.bfloat16, device=device)
+    ops.grouped_gemm(a.to(device)[:, k:2 * k], b.to(device), seg, e, m=m, out=out[:, 40:88])
+    ref = _ref_grouped(a[:, k:2 * k].float(), b, counts)
+    assert rel(out[:, 40:88], ref) < 1e-2
+    assert torch.count_nonzero(out[:, :40]) == 0 and torch.count_nonzero(out[:, 88:]) == 0
+
+
+@pytest.mark.parametrize("e,m,f,h,kt,gather", [(8, 1200, 512, 256, 32, True), (128, 4096, 768, 2048, 32, False)])
+def test_fc1_swiglu(device, e, m, f, h, kt, gather):
+    ops = _ops()
+    print(f"fc1_swiglu e={e} m={m} f={f} h={h}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    counts = _counts(e, m, seed=3)
+    t_src = 700
+    x = torch.randn(t_src if gather else m, h, generator=g).to(torch.bfloat16)
+    rows = torch.randint(0, t_src, (m,), generator=g, dtype=torch.int32) if gather else None
+    w1 = (torch.randn(e, 2 * f, h, generator=g) * 0.02).to(torch.bfloat16)
+    tl = torch.randn(m, kt, generator=g).to(torch.bfloat16)
+    l1 = (torch.randn(e, 2 * f, kt, generator=g) * 0.05).to(torch.bfloat16)
+    prob = torch.rand(m, generator=g)
+    seg = ops.segments_from_counts(counts, e, device)
+    y1, hh = ops.fc1_swiglu(x.to(device), w1.to(device), seg, e, prob.to(device), m=m,
+                            a_rows=rows.to(device) if gather else None, tl=tl.to(device),
+                            l1=l1.to(device))
+    torch.cuda.synchronize()
+    a_f = (x[rows.long()] if gather else x).float()
+    y1_ref = _ref_grouped(a_f, w1, counts, tl, l1)
+    assert rel(y1, y1_ref) < 1e-2
+    gg, uu = y1.cpu().float().chunk(2, dim=1)
+    h_ref = torch.nn.functional.silu(gg) * uu * prob[:, None]
+    assert rel(hh, h_ref) < 1e-2
+
+
+@pytest.mark.parametrize("e,m,f,h,kt", [(8, 1000, 512, 256, 16), (128, 4096, 768, 2048, 16)])
+def test_fc2_dgrad_swiglu(device, e, m, f, h, kt):
+    ops = _ops()
+    print(f"fc2_dgrad_swiglu e={e} m={m} f={f} h={h}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    counts = _counts(e, m, seed=4)
+    t_src = 600
+    dy = torch.randn(t_src, h, generator=g).to(torch.bfloat16)
+    rows = torch.randint(0, t_src, (m,), generator=g, dtype=torch.int32)
+    w2 = (torch.randn(e, h, f, generator=g) * 0.02).to(torch.bfloat16)
+    w2t = w2.transpose(1, 2).contiguous()
+    tl = torch.randn(m, kt, generator=g).to(torch.bfloat16)
+    l2 = (torch.randn(e, f, kt, generator=g) * 0.05).to(torch.bfloat16)
+    y1 = torch.randn(m, 2 * f, generator=g).to(torch.bfloat16)
+    prob = torch.rand(m, generator=g)
+    seg = ops.segments_from_counts(counts, e, device)
+    dy1, dp_part = ops.fc2_dgrad_swiglu(dy.to(device), w2t.to(device), seg, e, y1.to(device),
+                                        prob.to(device), m=m, a_rows=rows.to(device),
+                                        tl=tl.to(device), l2=l2.to(device))
+    torch.cuda.synchronize()
+    dh = _ref_grouped(dy[rows.long()].float(), w2t, counts, tl, l2)
+    y1f = y1.float().requires_grad_()
+    p = prob.clone().requires_grad_()
+    gg, uu = y1f.chunk(2, dim=1)
+    hh = torch.nn.functional.silu(gg) * uu * p[:, None]
+    hh.backward(dh)
+    assert rel(dy1, y1f.grad) < 1e-2
+    assert rel(dp_part.sum(0), p.grad) < 1e-3
+
+
+@pytest.mark.parametrize("e,m,p,q,gather,transpose", [
+    (8, 1000, 256, 16, True, False), (128, 4096, 2048, 32, False, False),
+    (16, 2000, 768, 16, False, True), (4, 300, 64, 128, True, True), (6, 500, 96, 48, False, False)])
+def test_grouped_wgrad(device, e, m, p, q, gather, transpose):
+    ops = _ops()
+    print(f"wgrad e={e} m={m} p={p} q={q}", flush=True)
+    g = torch.Generator().manual_seed(p + q)
+    counts = _counts(e, m, seed=9)
+    t_src = 400
+    lm = torch.randn(t_src if gather else m, p, generator=g).to(torch.bfloat16)
+    rows = torch.randint(0, t_src, (m,), generator=g, dtype=torch.int32) if gather else None
+    r = torch.randn(m, q, generator=g).to(torch.bfloat16)
+    seg = ops.segments_from_counts(counts, e, device)
+    got = ops.grouped_wgrad(lm.to(device), r.to(device), seg, e, alpha=2.0,
+                            l_rows=rows.to(device) if gather else None, transpose_out=transpose)
+    torch.cuda.synchronize()
+    lf = (lm[rows.long()] if gather else lm).float()
+    ref = torch.zeros(e, p, q)
+    cur = 0
+    for i, c in enumerate(counts):
+        ref[i] = 2.0 * lf[cur:cur + c].t() @ r[cur:cur + c].float()
+        cur += c
+    if transpose:
+        ref = ref.transpose(1, 2)
+    assert rel(got, ref) < 1e-5, rel(got, ref)
+    for i, c in enumerate(counts):
+        if c == 0:
+            assert torch.count_nonzero(got[i]) == 0
+
+
+def test_transpose(device):
+    ops = _ops()
+    src = torch.randn(3, 70, 45).to(torch.bfloat16)
+    got = ops.transposed(src.to(device), 2.0)
+    assert torch.equal(got.cpu(), (src.float() * 2).transpose(1, 2).to(torch.bfloat16))

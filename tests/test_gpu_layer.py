@@ -1,0 +1,148 @@
+"""GPU parity of the fused MoE-LoRA expert layer (forward + backward) against the
+CPU oracle (oracle/layer.py, fp32 autograd of the reference torch path).
+
+Bar (from the specification): routing indices / counts bit-exact; outputs, dx
+and LoRA gradients within 2e-2 norm-relative (bf16 path vs fp32 oracle);
+router logits within 1e-5.
+Full-size checks use token locality: each output row and each dx row depends
+only on its own token, and the LoRA gradients are linear in dy, so driving dy
+on a token subset S lets the oracle run on S alone; dx outside S must be 0.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import layer as OL
+from oracle import routing as R
+
+pytestmark = pytest.mark.gpu
+NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
+
+
+def rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _gpu_layer(inp, device, *, use_logits, use_target, dy=None):
+    from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
+    cfg = inp.cfg
+    base = FrozenExperts.build(inp.w_r.to(device), inp.w1.to(device), inp.w2.to(device))
+    lora = {n: inp.lora[n].to(device).requires_grad_() for n in NAMES}
+    x = inp.x.to(device).requires_grad_()
+    logits = inp.logits.to(device).requires_grad_() if use_logits else None
+    target = inp.target.to(device) if use_target else None
+    s = cfg.scale
+    y, idx, counts, status = moe_lora_layer(x, base, *(lora[n] for n in NAMES), k=cfg.k,
+                                            scales=(s, s, s), logits=logits, target=target)
+    y.backward((inp.dy if dy is None else dy).to(device))
+    torch.cuda.synchronize()
+    out = {"y": y.detach().cpu(), "idx": idx.cpu(), "counts": counts.cpu(), "status": int(status.item()),
+           "dx": x.grad.cpu()}
+    if use_logits:
+        out["dlogits"] = logits.grad.cpu()
+    for n in NAMES:
+        out["d" + n] = lora[n].grad.cpu()
+    return out
+
+
+def _oracle_layer(inp, *, tokens=None, logits_given, target, dy=None):
+    cfg = inp.cfg
+    sel = slice(None) if tokens is None else tokens
+    x = inp.x[sel].float().requires_grad_()
+    leaves = {n: inp.lora[n].float().requires_grad_() for n in NAMES}
+    p = OL.LayerParams(w_r=None if logits_given else inp.w_r, w1=inp.w1, w2=inp.w2,
+                       scale_g=cfg.scale, scale_u=cfg.scale, scale_d=cfg.scale, **leaves)
+    logits = inp.logits[sel].float().requires_grad_() if logits_given else None
+    y, aux = OL.moe_lora_layer(x, p, cfg.k, logits=logits, target=target)
+    y.backward((inp.dy if dy is None else dy)[sel].float())
+    out = {"y": y.detach(), "dx": x.grad, "aux": aux}
+    if logits_given:
+        out["dlogits"] = logits.grad
+    for n in NAMES:
+        out["d" + n] = leaves[n].grad
+    return out
+
+
+def _compare(got, ref, keys, tol=2e-2):
+    for key in keys:
+        err = rel(got[key], ref[key])
+        print(f"  {key}: rel err {err:.2e}", flush=True)
+        assert err < tol, (key, err)
+
+
+def _small(cfg_name, T, replay=False):
+    from art_amd.workloads import CONFIGS, make_inputs
+    import dataclasses
+    cfg = CONFIGS[cfg_name]
+    if replay:
+        cfg = dataclasses.replace(cfg, replay=True)
+    return make_inputs(cfg, "cpu", seed=0, T=T)
+
+
+def test_layer_c0_given_logits(device):
+    """C0 (T=256, H=256, E=8, k=2, F=512, r=8, alpha=16) with given fp32 logits."""
+    from art_amd.workloads import CONFIGS
+    print("layer C0 given logits", flush=True)
+    inp = _small("C0", 256)
+    inp.logits = torch.randn(256, 8, generator=torch.Generator().manual_seed(5))
+    got = _gpu_layer(inp, device, use_logits=True, use_target=False)
+    ref = _oracle_layer(inp, logits_given=True, target=None)
+    assert np.array_equal(got["idx"].numpy(), ref["aux"]["idx"].numpy())
+    assert got["counts"].tolist() == ref["aux"]["plan"]["counts"].tolist()
+    _compare(got, ref, ["y", "dx", "dlogits"] + ["d" + n for n in NAMES])
+
+
+def test_layer_c0_router_weights(device):
+    """C0 with the router gating linear on the GPU: logits within 1e-5; the
+    oracle then replays the GPU's selection (near-ties may legitimately differ)."""
+    from art_amd.megatron.moe_layer import router_logits
+    print("layer C0 router", flush=True)
+    inp = _small("C0", 256)
+    lg = router_logits(inp.x.to(device), inp.w_r.to(device)).cpu()
+    lg_ref = OL.router_logits(inp.x, inp.w_r)
+    assert rel(lg, lg_ref) < 1e-5
+    got = _gpu_layer(inp, device, use_logits=False, use_target=False)
+    ref = _oracle_layer(inp, logits_given=False, target=got["idx"].long())
+    # the GPU's selection is the top-k of its own logits, bit-exact
+    assert np.array_equal(got["idx"].numpy(), R.topk_indices(lg.numpy(), inp.cfg.k))
+    _compare(got, ref, ["y", "dx"] + ["d" + n for n in NAMES])
+
+
+def test_layer_c2_replay_small(device):
+    """C2-style Zipf replay (T=512, full Qwen widths): empty experts, ragged segments."""
+    print("layer C2 replay T=512", flush=True)
+    inp = _small("C2", 512, replay=True)
+    got = _gpu_layer(inp, device, use_logits=True, use_target=True)
+    assert got["status"] == 0
+    assert np.array_equal(got["idx"].numpy(), inp.target.numpy())
+    ref = _oracle_layer(inp, logits_given=True, target=inp.target)
+    assert got["counts"].tolist() == ref["aux"]["plan"]["counts"].tolist()
+    assert (got["counts"] == 0).any()
+    _compare(got, ref, ["y", "dx", "dlogits"] + ["d" + n for n in NAMES])
+
+
+def test_layer_c1_full_size_token_subset(device):
+    """Full C1 (T=8192) on the GPU; dy on 48 tokens; the oracle runs on those tokens."""
+    from art_amd.workloads import CONFIGS, make_inputs
+    print("layer C1 full size", flush=True)
+    cfg = CONFIGS["C1"]
+    inp = make_inputs(cfg, "cpu", seed=0)
+    gen = torch.Generator().manual_seed(9)
+    subset = torch.randperm(cfg.T, generator=gen)[:48].sort().values
+    dy = torch.zeros_like(inp.dy)
+    dy[subset] = inp.dy[subset]
+    got = _gpu_layer(inp, device, use_logits=False, use_target=False, dy=dy)
+    counts = got["counts"]
+    assert int(counts.sum()) == cfg.T * cfg.k
+    # routing: bit-exact top-k of the GPU logits is checked in the C0 test; here
+    # the expert histogram must match the selection
+    assert counts.tolist() == np.bincount(got["idx"].numpy().reshape(-1), minlength=cfg.E).tolist()
+    outside = torch.ones(cfg.T, dtype=torch.bool)
+    outside[subset] = False
+    assert torch.count_nonzero(got["dx"][outside]) == 0
+    ref = _oracle_layer(inp, tokens=subset, logits_given=False, target=got["idx"][subset].long(), dy=dy)
+    got_sub = dict(got)
+    got_sub["y"] = got["y"][subset]
+    got_sub["dx"] = got["dx"][subset]
+    _compare(got_sub, ref, ["y", "dx"] + ["d" + n for n in NAMES])

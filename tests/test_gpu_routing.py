@@ -1,0 +1,163 @@
+"""GPU parity of the routing family: top-k, replay, dispatch plan, permute, combine.
+
+Bar: bit-exact indices / counts / offsets / destination rows / row->token maps
+against the CPU oracle (oracle/routing.py), at the full C1/C2 sizes and on the
+reference's own KAT routes; weights within 1e-6 of the oracle's softmax.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import routing as R
+
+pytestmark = pytest.mark.gpu
+KATS = json.loads((Path(__file__).parent / "golden" / "routing_kats.json").read_text())
+
+
+def _ops():
+    from art_amd import ops
+    return ops
+
+
+def _seg_expect(counts, e):
+    counts = np.asarray(counts, dtype=np.int64)
+    rows = [np.concatenate([[0], np.cumsum(counts)])]
+    for b in range(4):
+        bm = 32 << b
+        rows.append(np.concatenate([[0], np.cumsum((counts + bm - 1) // bm)]))
+    return np.concatenate(rows)
+
+
+def _check_plan(plan, idx_np, e, w=None):
+    exp = R.dispatch_plan(idx_np, e)
+    m = idx_np.size
+    assert plan.counts.cpu().tolist() == exp["counts"].tolist()
+    assert plan.seg.cpu().numpy().tolist() == _seg_expect(exp["counts"], e).tolist()
+    assert np.array_equal(plan.dest.cpu().numpy(), exp["dest"])
+    assert np.array_equal(plan.row_token.cpu().numpy()[:m], exp["row_token"])
+    if w is not None:
+        rp = plan.row_prob.cpu().numpy()
+        assert np.array_equal(rp, w.reshape(-1)[exp["row_token"] * idx_np.shape[1] + exp["row_slot"]])
+    assert int(plan.status.item()) == 0
+
+
+@pytest.mark.parametrize("t,e,k", [(8192, 128, 8), (256, 8, 2), (1000, 64, 6), (3, 5, 5), (130, 300, 4)])
+def test_topk_softmax_bit_exact(device, t, e, k):
+    ops = _ops()
+    print(f"topk t={t} e={e} k={k}", flush=True)
+    g = torch.Generator().manual_seed(t + e + k)
+    logits = torch.randn(t, e, generator=g)
+    logits[0, : min(4, e)] = 0.5  # exact ties
+    idx, w = ops.router_topk(logits.to(device), k)
+    torch.cuda.synchronize()
+    exp_idx, exp_w = R.topk_softmax(logits.numpy(), k)
+    assert np.array_equal(idx.cpu().numpy(), exp_idx)
+    np.testing.assert_allclose(w.cpu().numpy(), exp_w, rtol=2e-6, atol=1e-7)
+
+
+def test_topk_tie_rule_kats(device):
+    ops = _ops()
+    for case in KATS["topk_tie_rule"]:
+        row = torch.tensor([[float(v) for v in case["logits"]]], dtype=torch.float32)
+        idx, _ = ops.router_topk(row.to(device), case["k"])
+        assert idx.cpu()[0].tolist() == case["idx"], case
+    for case in KATS["softmax_closed_form"]:
+        row = torch.tensor([case["logits"]], dtype=torch.float32)
+        idx, w = ops.router_topk(row.to(device), case["k"])
+        assert idx.cpu()[0].tolist() == case["idx"]
+        np.testing.assert_allclose(w.cpu()[0].numpy(), case["w"], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("name", ["replay_bundle_E3_k2", "sampled_bundle_call0", "sampled_bundle_call1"])
+def test_replay_and_plan_reference_kats(device, name):
+    ops = _ops()
+    kat = KATS[name]
+    target = torch.tensor(kat["routes"], dtype=torch.int64)
+    t, k = target.shape
+    e = kat["num_experts"]
+    logits = torch.randn(t, e, generator=torch.Generator().manual_seed(3))
+    idx, w, status = ops.router_replay(logits.to(device), target.to(device))
+    assert int(status.item()) == 0
+    assert idx.cpu().tolist() == kat["routes"]
+    plan = ops.dispatch_plan(idx, w, e)
+    assert plan.counts.cpu().tolist() == kat["counts"]
+    assert plan.offsets.cpu().tolist() == kat["offsets"]
+    assert plan.row_token.cpu().tolist() == kat["row_token"]
+    assert plan.dest.cpu().tolist() == kat["dest"]
+
+
+def test_replay_zipf_c2_bit_exact(device):
+    from art_amd.workloads import CONFIGS, make_inputs
+    ops = _ops()
+    cfg = CONFIGS["C2"]
+    inp = make_inputs(cfg, "cpu", seed=0)
+    print("replay C2 full size", flush=True)
+    idx, w, status = ops.router_replay(inp.logits.to(device), inp.target.to(device))
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    assert np.array_equal(idx.cpu().numpy(), inp.target.numpy().astype(np.int32))
+    exp_idx, exp_w = R.replay(inp.logits.numpy(), inp.target.numpy())
+    np.testing.assert_allclose(w.cpu().numpy(), exp_w, rtol=2e-6, atol=1e-7)
+    plan = ops.dispatch_plan(idx, w, cfg.E)
+    counts = plan.counts.cpu().numpy()
+    assert (counts == 0).any(), "Zipf(1.2) replay should leave some experts empty"
+    _check_plan(plan, exp_idx, cfg.E, w.cpu().numpy())
+
+
+def test_replay_rejects_out_of_range_and_repeated_ids(device):
+    ops = _ops()
+    logits = torch.randn(3, 4)
+    target = torch.tensor([[0, 4], [1, 1], [2, 3]])
+    idx, w, status = ops.router_replay(logits.to(device), target.to(device))
+    assert int(status.item()) == 2
+    assert idx.cpu().tolist() == [[0, -1], [1, -1], [2, 3]]
+    assert w.cpu()[0, 1].item() == 0.0 and abs(w.cpu()[0, 0].item() - 1.0) < 1e-6
+    plan = ops.dispatch_plan(idx, w, 4)
+    assert plan.counts.cpu().tolist() == [1, 1, 1, 1]
+    assert plan.dest.cpu().tolist() == [[0, -1], [1, -1], [2, 3]]
+    assert int(plan.status.item()) == 2  # the two rejected slots again
+
+
+@pytest.mark.parametrize("t,e,k", [(8192, 128, 8), (0, 8, 2), (1, 4, 4), (64, 1, 1), (4097, 256, 8)])
+def test_dispatch_plan_bit_exact(device, t, e, k):
+    ops = _ops()
+    print(f"plan t={t} e={e} k={k}", flush=True)
+    rng = np.random.default_rng(t * 7 + e)
+    idx = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int32) \
+        if t else np.zeros((0, k), np.int32)
+    w = rng.random((t, k)).astype(np.float32)
+    plan = ops.dispatch_plan(torch.from_numpy(idx).to(device), torch.from_numpy(w).to(device), e)
+    torch.cuda.synchronize()
+    _check_plan(plan, idx, e, w)
+
+
+def test_segments_from_counts(device):
+    ops = _ops()
+    counts = [32, 0, 16, 24, 0, 300, 1]
+    seg = ops.segments_from_counts(counts, len(counts), device)
+    assert seg.cpu().numpy().tolist() == _seg_expect(counts, len(counts)).tolist()
+
+
+@pytest.mark.parametrize("t,h,e,k", [(8192, 2048, 128, 8), (33, 256, 8, 2), (5, 8, 4, 3)])
+def test_permute_and_combine_bit_exact(device, t, h, e, k):
+    ops = _ops()
+    print(f"permute/combine t={t} h={h}", flush=True)
+    rng = np.random.default_rng(h)
+    idx = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int32)
+    plan = ops.dispatch_plan(torch.from_numpy(idx).to(device), None, e)
+    x = torch.randn(t, h, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    xp = ops.permute(x.to(device), plan.dest, t * k)
+    exp = R.dispatch_plan(idx, e)
+    assert torch.equal(xp.cpu(), x[torch.from_numpy(exp["row_token"])])
+    # combine: fp32 sum over j in slot order, rounded once to bf16
+    yp = torch.randn(t * k, h, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    wgt = torch.rand(t, k, generator=torch.Generator().manual_seed(4))
+    y = ops.combine(yp.to(device), plan.dest, t, wgt=wgt.to(device))
+    dest = torch.from_numpy(exp["dest"])
+    acc = torch.zeros(t, h, dtype=torch.float32)
+    for j in range(k):
+        acc = acc + wgt[:, j:j + 1] * yp[dest[:, j]].float()
+    assert torch.equal(y.cpu(), acc.to(torch.bfloat16))

@@ -1,0 +1,126 @@
+"""Pins the routing oracle (oracle/routing.py) against known answers and brute force.
+
+CPU only.  Nothing here computes the expected value with the oracle's own
+formula: the checks are the hand-derived KATs of tests/golden/routing_kats.json
+(from the reference's unit-test inputs), Python ``sorted()`` brute force,
+megatron's own masked_select construction, and softmax closed forms.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import scipy.special
+
+from oracle import routing as R
+
+KATS = json.loads((Path(__file__).parent / "golden" / "routing_kats.json").read_text())
+
+
+def _f(v):
+    return float(v) if not isinstance(v, str) else float(v.replace("inf", "inf"))
+
+
+@pytest.mark.parametrize("name", ["replay_bundle_E3_k2", "sampled_bundle_call0", "sampled_bundle_call1"])
+def test_dispatch_plan_matches_reference_kat(name):
+    kat = KATS[name]
+    idx = np.array(kat["routes"], dtype=np.int32)
+    plan = R.dispatch_plan(idx, kat["num_experts"])
+    assert plan["counts"].tolist() == kat["counts"]
+    assert plan["offsets"].tolist() == kat["offsets"]
+    assert plan["row_token"].tolist() == kat["row_token"]
+    assert plan["dest"].tolist() == kat["dest"]
+    if "routing_map" in kat:
+        assert R.routing_map_from_idx(idx, kat["num_experts"]).astype(int).tolist() == kat["routing_map"]
+
+
+def _brute_topk(row, k):
+    def key(i):
+        v = row[i]
+        nan = math.isnan(v)
+        return (0 if nan else 1, 0.0 if nan else -(v + 0.0), i)
+    return sorted(range(len(row)), key=key)[:k]
+
+
+def test_topk_tie_rule_kats():
+    for case in KATS["topk_tie_rule"]:
+        row = np.array([_f(v) for v in case["logits"]], dtype=np.float32)
+        got = R.topk_indices(row[None, :], case["k"])[0].tolist()
+        assert got == case["idx"], case
+        assert _brute_topk(row.tolist(), case["k"]) == case["idx"]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_topk_matches_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    logits = rng.standard_normal((64, 12)).astype(np.float32)
+    # plant exact ties and a NaN
+    logits[3, 4] = logits[3, 7]
+    logits[9, :] = 1.0
+    logits[11, 2] = np.nan
+    idx = R.topk_indices(logits, 5)
+    for t in range(logits.shape[0]):
+        assert idx[t].tolist() == _brute_topk(logits[t].tolist(), 5)
+
+
+def test_softmax_closed_forms():
+    for case in KATS["softmax_closed_form"]:
+        logits = np.array([case["logits"]], dtype=np.float32)
+        idx, w = R.topk_softmax(logits, case["k"])
+        assert idx[0].tolist() == case["idx"]
+        np.testing.assert_allclose(w[0], case["w"], rtol=1e-6, atol=1e-7)
+
+
+def test_softmax_ratio_and_scipy():
+    rng = np.random.default_rng(7)
+    logits = rng.standard_normal((200, 32)).astype(np.float32) * 3
+    idx, w = R.topk_softmax(logits, 6)
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+    sel = np.take_along_axis(logits.astype(np.float64), idx.astype(np.int64), 1)
+    np.testing.assert_allclose(np.log(w[:, 0] / w[:, 1]), sel[:, 0] - sel[:, 1], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(w, scipy.special.softmax(sel, axis=1), rtol=1e-6, atol=1e-7)
+    # descending
+    assert np.all(np.diff(sel, axis=1) <= 0)
+
+
+@pytest.mark.parametrize("seed,t,e,k", [(0, 50, 8, 2), (1, 300, 128, 8), (2, 7, 3, 3), (3, 1, 5, 1)])
+def test_dispatch_plan_matches_closed_form_and_loop(seed, t, e, k):
+    rng = np.random.default_rng(seed)
+    idx = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int32)
+    plan = R.dispatch_plan(idx, e)
+    rmap = R.routing_map_from_idx(idx, e)
+    # megatron's construction: arange(T).expand(E, T).masked_select(routing_map.T)
+    assert plan["row_token"].tolist() == R.row_token_closed_form(rmap).tolist()
+    assert plan["counts"].tolist() == rmap.sum(0).tolist()
+    # pure-Python loop: expert-major, token ascending
+    rows = []
+    for ee in range(e):
+        for tt in range(t):
+            if ee in idx[tt].tolist():
+                rows.append((tt, idx[tt].tolist().index(ee)))
+    for pos, (tt, jj) in enumerate(rows):
+        assert plan["dest"][tt, jj] == pos
+        assert plan["row_token"][pos] == tt
+        assert plan["row_slot"][pos] == jj
+
+
+def test_dispatch_plan_zero_tokens_and_empty_experts():
+    plan = R.dispatch_plan(np.zeros((0, 2), dtype=np.int32), 4)
+    assert plan["counts"].tolist() == [0, 0, 0, 0]
+    assert plan["offsets"].tolist() == [0, 0, 0, 0, 0]
+    idx = np.array([[3, 1], [1, 3]], dtype=np.int32)
+    plan = R.dispatch_plan(idx, 5)
+    assert plan["counts"].tolist() == [0, 2, 0, 2, 0]
+    assert plan["offsets"].tolist() == [0, 0, 2, 2, 4, 4]
+
+
+def test_replay_rejects_bad_ids():
+    logits = np.zeros((2, 4), dtype=np.float32)
+    with pytest.raises(ValueError):
+        R.replay(logits, np.array([[0, 4], [1, 2]]))
+    with pytest.raises(ValueError):
+        R.replay(logits, np.array([[0, 0], [1, 2]]))
+    idx, w = R.replay(logits, np.array([[3, 1], [0, 2]]))
+    assert idx.tolist() == [[3, 1], [0, 2]]
+    np.testing.assert_allclose(w, 0.5)
