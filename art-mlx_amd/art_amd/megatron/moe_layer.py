@@ -35,8 +35,8 @@ from typing import Any
 
 import torch
 
-from ... import ops
-from ..kernels.grouped_lora_hip import apply_operand, pad_rank_last, pad_rank_mid, padded_rank, proj_operand
+from .. import ops
+from .kernels.grouped_lora_hip import apply_operand, pad_rank_last, pad_rank_mid, padded_rank, proj_operand
 
 
 @dataclass

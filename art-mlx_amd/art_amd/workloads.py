@@ -15,11 +15,15 @@ router weight is ~ N(0, 1/H) so that the router logits x W_r^T are ~ N(0,1)
 is alpha / r with alpha = 32 (ART's LORA_ALPHA,
 /root/reference/src/art/megatron/lora.py:40) unless the config says otherwise.
 
-C2 replay targets: for each token, k distinct experts drawn without
-replacement with p(expert e) proportional to (e+1)^-1.2; the replayed gate
-weights are a Dirichlet(1) sample per token, realised by setting the logits of
-the selected experts to log(weight) (softmax over the selected logits then
-returns exactly those weights).
+C2 replay targets: experts get Zipf ranks 1..E through a seeded permutation;
+for each token, k distinct experts are drawn without replacement with
+p(rank i) proportional to i^-1.2.  Because k distinct draws per token reach
+every expert of a 128-way Zipf(1.2) within a few thousand tokens, the E/16
+lowest-ranked experts get probability 0, which realises the configuration's
+"some experts with 0 tokens".  The replayed gate weights are a Dirichlet(1)
+sample per token, realised by setting the logits of the selected experts to
+log(weight) (softmax over the selected logits then returns exactly those
+weights).
 """
 from __future__ import annotations
 
@@ -80,10 +84,23 @@ CONFIGS = {
 }
 
 
-def zipf_targets(t: int, e: int, k: int, s: float = 1.2, seed: int = 0) -> torch.Tensor:
-    """k distinct experts per token, p(e) ~ (e+1)^-s, without replacement (CPU, int64)."""
+def zipf_targets(t: int, e: int, k: int, s: float = 1.2, seed: int = 0,
+                 n_empty: int | None = None) -> torch.Tensor:
+    """k distinct experts per token, p(rank i) ~ i^-s without replacement (CPU, int64).
+
+    The expert of rank i is perm[i-1] for a seeded permutation; the ``n_empty``
+    (default E/16) lowest-ranked experts get probability 0.
+    """
     g = torch.Generator().manual_seed(seed)
-    p = torch.arange(1, e + 1, dtype=torch.float64).pow(-s)
+    perm = torch.randperm(e, generator=g)
+    n_empty = max(1, e // 16) if n_empty is None else n_empty
+    if e - n_empty < k:
+        raise ValueError("not enough experts with non-zero probability for k distinct draws")
+    p_rank = torch.arange(1, e + 1, dtype=torch.float64).pow(-s)
+    if n_empty:
+        p_rank[e - n_empty:] = 0.0
+    p = torch.zeros(e, dtype=torch.float64)
+    p[perm] = p_rank
     p = (p / p.sum()).float()
     out = torch.empty((t, k), dtype=torch.int64)
     chunk = 4096

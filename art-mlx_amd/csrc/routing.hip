@@ -300,14 +300,18 @@ __global__ __launch_bounds__(256) void combine_kernel(
   const float my_w = (act && wgt) ? wgt[t * k + lane] : 1.0f;
   const int my_e = (act && w_r) ? idx[t * k + lane] : -1;
   const float my_dl = (act && w_r) ? dl[t * k + lane] : 0.0f;
-  for (int c = lane; c < H8; c += kWave) {
+  // The chunk loop is uniform across the wavefront (every lane runs every
+  // iteration) so that the slot broadcasts below always read active lanes.
+  for (int c0 = 0; c0 < H8; c0 += kWave) {
+    const int c = c0 + lane;
+    const bool on = c < H8;
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
     for (int j = 0; j < k; ++j) {
       const int d = __shfl(my_dest, j, kWave);
       const float wj = __shfl(my_w, j, kWave);
-      if (d < 0) continue;
+      if (d < 0 || !on) continue;
       float f[8];
       unpack8(yp[(int64_t)d * H8 + c], f);
 #pragma unroll
@@ -317,14 +321,14 @@ __global__ __launch_bounds__(256) void combine_kernel(
       for (int j = 0; j < k; ++j) {
         const int e = __shfl(my_e, j, kWave);
         const float lj = __shfl(my_dl, j, kWave);
-        if (e < 0) continue;
+        if (e < 0 || !on) continue;
         float f[8];
         unpack8(w_r[(int64_t)e * H8 + c], f);
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] += lj * f[i];
       }
     }
-    y[t * H8 + c] = pack8(acc);
+    if (on) y[t * H8 + c] = pack8(acc);
   }
 }
 
