@@ -16,11 +16,22 @@
 // workgroup -> tile order is remapped so that each of the 8 XCDs works on a
 // contiguous run of tiles (shared A rows / expert weights stay in its L2).
 //
-// Tiles: BM x BN per workgroup, BK = 64, WM x WN wavefronts, each wave owning
-// (BM/WM) x (BN/WN) in 32x32 blocks of v_mfma_f32_32x32x16_bf16.  LDS holds
-// two stages of A and B; 16-byte chunks are XOR-swizzled by row so that both
-// the global->LDS stores and the MFMA operand reads are bank-conflict free.
-// Global loads of stage k+1 are issued before the MFMAs of stage k.
+// Main loop: BM x BN x 64 tiles, WM x WN wavefronts, each wave owning
+// (BM/WM) x (BN/WN) in 32x32 blocks of v_mfma_f32_32x32x16_bf16.  Operand
+// tiles move global -> LDS with global_load_lds_dwordx4 (no VGPR staging)
+// into a STAGES-deep ring; stage k+STAGES-1 is in flight while stage k is
+// multiplied, with one workgroup barrier per k-step.  Each lane's DMA slot is
+// fixed (lane i of an instruction fills bytes 16i..16i+15 of a 1 KB block =
+// 8 rows x 64 bf16), so the XOR swizzle of 16-byte chunks by row is applied to
+// the global addresses.  Rows past the segment or N, and k-chunks past K, are
+// clamped to valid addresses; the rows' results are never stored and partial
+// k-tiles run only their valid 16-wide MFMA steps, so no branch guards a load.
+//
+// The MFMA is issued with B as its first operand, so a lane's accumulators
+// hold 4 consecutive output columns of one row; epilogues pack them to bf16,
+// stage the tile through the (now idle) LDS ring and write 16-byte chunks.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace art {
@@ -52,29 +63,127 @@ struct NTArgs {
   // SwiGLU
   int F;
   const float *prob;
-  bf16 *y1;      // fwd out [M][2F]
-  bf16 *h;       // fwd out [M][F]
+  bf16 *y1;           // fwd out [M][2F]
+  bf16 *h;            // fwd out [M][F]
   const bf16 *y1_in;  // bwd in [M][2F]
-  bf16 *dy1;     // bwd out [M][2F]
-  float *dp_part;  // bwd out [n_tiles][M]
+  bf16 *dy1;          // bwd out [M][2F]
+  float *dp_part;     // bwd out [ceil(F/128)][M]
   int64_t M;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ (row & 7)) * 8; }
+typedef __attribute__((address_space(3))) void *lds_void_ptr;
 
-template <int BM, int BN, int WM, int WN, int EPI>
+__device__ __forceinline__ void dma16(const bf16 *g, void *lds) {
+  __builtin_amdgcn_global_load_lds((const void *)g, (lds_void_ptr)lds, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier that waits for this wave's LDS reads/writes (lgkmcnt) but
+// not for its global loads: in-flight LDS-DMA prefetches of later stages stay
+// outstanding (a fenced __syncthreads would drain them with vmcnt(0)).
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+  return make_uint2(pack2(a, b), pack2(c, d));
+}
+
+// 16-byte chunk swizzle of a 128-byte LDS row (64 bf16): logical chunk c of
+// row r lives at physical chunk c ^ swz(r).  Any 8 consecutive rows, and any 16
+// consecutive rows taken with their parity, hit distinct bank groups, so the
+// MFMA operand reads (32 lanes on 32 consecutive rows) are conflict-free for
+// both a 32-bank (8 lanes x 16 B per cycle) and a 64-bank (16 lanes) LDS.
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// One stage of operand DMA for this wave: A_PW blocks of A rows, B_PW of B rows.
+template <int A_PW, int B_PW, int A_BYTES>
+__device__ __forceinline__ void issue_stage(char *st, int wave, const char *abase,
+                                            const char *bbase, const uint32_t (&aoff)[A_PW],
+                                            const uint32_t (&boff)[B_PW], uint32_t sh) {
+#pragma unroll
+  for (int i = 0; i < A_PW; ++i)
+    dma16((const bf16 *)(abase + (aoff[i] + sh)), st + (wave * A_PW + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i)
+    dma16((const bf16 *)(bbase + (boff[i] + sh)), st + A_BYTES + (wave * B_PW + i) * 1024);
+}
+
+// Stage DMA for a partial k-tile: a chunk past klim re-reads the row's last
+// chunk (those columns are never multiplied).  The logical chunk of block b's
+// slot is (lane & 7) ^ swz(8b + lane / 8).
+template <int A_PW, int B_PW, int A_BYTES>
+__device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, const char *abase,
+                                                 const char *bbase, const uint32_t (&aoff)[A_PW],
+                                                 const uint32_t (&boff)[B_PW], int kb, int klim) {
+#pragma unroll
+  for (int i = 0; i < A_PW; ++i) {
+    const int bi = wave * A_PW + i;
+    const int ch = (lane & 7) ^ swz(bi * 8 + (lane >> 3));
+    const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
+    dma16((const bf16 *)(abase + (aoff[i] + (uint32_t)(off * 2))), st + bi * 1024);
+  }
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int bi = wave * B_PW + i;
+    const int ch = (lane & 7) ^ swz(bi * 8 + (lane >> 3));
+    const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
+    dma16((const bf16 *)(bbase + (boff[i] + (uint32_t)(off * 2))), st + A_BYTES + bi * 1024);
+  }
+}
+
+// MFMA operands of one 16-wide k step from a swizzled stage (rows of 64 bf16).
+template <int TM, int TN, int WTM, int WTN, int A_BYTES>
+__device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int wn, int lrow, int lk,
+                                           bf16x8 (&af)[TM], bf16x8 (&bfv)[TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = wm * WTM + i * 32 + lrow;
+    af[i] = *(const bf16x8 *)(st + r * 128 + (((kk * 2 + lk) ^ swz(r)) << 4));
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int r = wn * WTN + j * 32 + lrow;
+    bfv[j] = *(const bf16x8 *)(st + A_BYTES + r * 128 + (((kk * 2 + lk) ^ swz(r)) << 4));
+  }
+}
+
+// B is the MFMA's first operand: acc[i][j] accumulates the transposed block,
+// so each lane ends up with 4 consecutive output columns of one row.
+template <int TM, int TN>
+__device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&af)[TM],
+                                         const bf16x8 (&bfv)[TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfv[j], af[i], acc[i][j], 0, 0, 0);
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int BK = 64;
-  constexpr int NT = WM * WN * 64;
+  constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int CA = BM * 8 / NT, CB = BN * 8 / NT;  // 16-byte chunks per thread
-  static_assert(TM >= 1 && TN >= 1 && CA >= 1 && CB >= 1, "tile config");
+  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  constexpr int A_PW = BM / 8 / NW, B_PW = BN / 8 / NW;  // 1 KB DMA blocks per wave
+  constexpr int G = A_PW + B_PW;                          // DMA instructions per stage per wave
+  constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+  constexpr int UMASK = (BN / 4 >= 32) ? 31 : (BN / 4 - 1);  // staging swizzle (8-byte units)
+  static_assert(TM >= 1 && TN >= 1 && A_PW >= 1 && B_PW >= 1, "tile config");
+  static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "DMA blocks must split across waves");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN % 2 == 0), "SwiGLU forward pairs gate/up blocks");
-  static_assert(NT % 8 == 0, "threads");
+  static_assert(BM * BN * 2 <= LDS_BYTES, "epilogue staging must fit the LDS ring");
+  static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 4, "vmcnt range");
+  static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
 
-  __shared__ __attribute__((aligned(16))) bf16 sA[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) bf16 sB[2][BN * BK];
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
   __shared__ float sRed[EPI == EPI_SWIGLU_BWD ? WN * BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -86,7 +195,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   const int lb = (nb % 8 == 0) ? ((blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3)) : blockIdx.x;
   const int nk_main = (p.K + BK - 1) / BK;
   const int nk = nk_main + (p.kt + BK - 1) / BK;
-  const int chunk = tid & 7;
+  const int nk_full = p.K / BK;  // full 64-wide k-tiles of the base product
+  // DMA slot of this lane inside a 1 KB block (8 rows): row lane/8, physical
+  // chunk lane%8, holding logical chunk (lane%8) ^ swz(row).
+  const int drow = lane >> 3;
 
   for (int tile = lb; tile < total; tile += nb) {
     const int mt = tile / n_tiles, nt = tile - mt * n_tiles;
@@ -99,69 +211,55 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     const int m0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
     const int m_end = p.seg_off[e + 1];
 
-    // Row pointers of this thread's A / Tl chunks and B / L chunks.
-    const bf16 *aptr[CA];
-    const bf16 *tptr[CA];
+    // Source rows of this lane's DMA slots (clamped into the segment / N), as
+    // 32-bit byte offsets from wave-uniform bases (the host checks that every
+    // operand spans less than 4 GiB).
+    const char *abase = (const char *)p.a;
+    const char *tbase = (const char *)(p.t ? p.t : p.a);
+    const char *bbase = (const char *)(p.b + (int64_t)e * p.b_es);
+    const char *lbase = p.l ? (const char *)(p.l + (int64_t)e * p.l_es) : bbase;
+    uint32_t aoff[A_PW], toff[A_PW], boff[B_PW], loff[B_PW];
 #pragma unroll
-    for (int i = 0; i < CA; ++i) {
-      const int r = (tid >> 3) + i * (NT / 8);
-      const int m = m0 + r;
-      if (m < m_end) {
-        const int64_t src = p.a_rows ? (int64_t)p.a_rows[m] : (int64_t)m;
-        aptr[i] = p.a + src * p.lda;
-        tptr[i] = p.t ? p.t + (int64_t)m * p.ldt : nullptr;
-      } else {
-        aptr[i] = nullptr;
-        tptr[i] = nullptr;
-      }
+    for (int i = 0; i < A_PW; ++i) {
+      int m = m0 + (wave * A_PW + i) * 8 + drow;
+      m = m < m_end ? m : m_end - 1;
+      const uint32_t src = p.a_rows ? (uint32_t)p.a_rows[m] : (uint32_t)m;
+      const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * A_PW + i) * 8 + drow));
+      aoff[i] = (src * (uint32_t)p.lda + ch * 8) * 2u;
+      toff[i] = ((uint32_t)m * (uint32_t)p.ldt + ch * 8) * 2u;
     }
-    const bf16 *bptr[CB];
-    const bf16 *lptr[CB];
 #pragma unroll
-    for (int i = 0; i < CB; ++i) {
-      const int r = (tid >> 3) + i * (NT / 8);
-      int n = nt * BN + r;
-      bool ok = n < p.N;
+    for (int i = 0; i < B_PW; ++i) {
+      const int r = (wave * B_PW + i) * 8 + drow;
+      int n;
       if (EPI == EPI_SWIGLU_FWD) {
         // logical 32-column blocks alternate gate / up of the same columns
-        const int blk = r >> 5, within = r & 31;
-        n = ((blk & 1) ? p.F : 0) + nt * (BN / 2) + (blk >> 1) * 32 + within;
-        ok = (nt * (BN / 2) + (blk >> 1) * 32 + within) < p.F;
+        const int blk = r >> 5;
+        int f = nt * (BN / 2) + (blk >> 1) * 32 + (r & 31);
+        f = f < p.F ? f : p.F - 1;
+        n = ((blk & 1) ? p.F : 0) + f;
+      } else {
+        n = nt * BN + r;
+        n = n < p.N ? n : p.N - 1;
       }
-      bptr[i] = ok ? p.b + (int64_t)e * p.b_es + (int64_t)n * p.ldb : nullptr;
-      lptr[i] = (ok && p.l) ? p.l + (int64_t)e * p.l_es + (int64_t)n * p.ldl : nullptr;
+      const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * B_PW + i) * 8 + drow));
+      boff[i] = ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
+      loff[i] = ((uint32_t)n * (uint32_t)p.ldl + ch * 8) * 2u;
     }
 
-    U4 ra[CA], rb[CB];
-    auto gload = [&](int ks) {
-      const bool main = ks < nk_main;
-      const int k0 = (main ? ks : ks - nk_main) * BK + chunk * 8;
-      const int klim = main ? p.K : p.kt;
-#pragma unroll
-      for (int i = 0; i < CA; ++i) {
-        const bf16 *s = main ? aptr[i] : tptr[i];
-        if (s && k0 < klim) ra[i] = *(const U4 *)(s + k0);
-        else ra[i] = U4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int i = 0; i < CB; ++i) {
-        const bf16 *s = main ? bptr[i] : lptr[i];
-        if (s && k0 < klim) rb[i] = *(const U4 *)(s + k0);
-        else rb[i] = U4{0u, 0u, 0u, 0u};
-      }
-    };
-    auto lstore = [&](int st) {
-#pragma unroll
-      for (int i = 0; i < CA; ++i) {
-        const int r = (tid >> 3) + i * (NT / 8);
-        *(U4 *)&sA[st][r * BK + swz(r, chunk)] = ra[i];
-      }
-#pragma unroll
-      for (int i = 0; i < CB; ++i) {
-        const int r = (tid >> 3) + i * (NT / 8);
-        *(U4 *)&sB[st][r * BK + swz(r, chunk)] = rb[i];
-      }
-    };
+#define ART_ISSUE(ks)                                                                         \
+  do {                                                                                        \
+    char *st_ = smem + ((ks) % STAGES) * STAGE_BYTES;                                         \
+    if ((ks) < nk_full)                                                                       \
+      issue_stage<A_PW, B_PW, A_BYTES>(st_, wave, abase, bbase, aoff, boff,                   \
+                                       (uint32_t)((ks) * BK * 2));                            \
+    else if ((ks) < nk_main)                                                                  \
+      issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, abase, bbase, aoff, boff,        \
+                                            (ks) * BK, p.K);                                  \
+    else                                                                                      \
+      issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, tbase, lbase, toff, loff,        \
+                                            ((ks) - nk_main) * BK, p.kt);                     \
+  } while (0)
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -171,151 +269,312 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    __syncthreads();  // previous tile's readers of stage 0 are done
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int ks = 0; ks < nk; ++ks) {
-      const int st = ks & 1;
-      if (ks + 1 < nk) gload(ks + 1);
+    barrier_nofence();  // the previous tile's epilogue no longer reads the ring
 #pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < nk) ART_ISSUE(s);
+
+    // Wait until stage ks has landed (at most min(STAGES-2, nk-1-ks) later
+    // groups may still be in flight), then release the slot ks+STAGES-1 reuses.
+#define ART_STAGE_IN(ks)                                                                      \
+  do {                                                                                        \
+    const int pend_ = (nk - 1 - (ks)) < (STAGES - 2) ? (nk - 1 - (ks)) : (STAGES - 2);        \
+    if (STAGES == 2 || pend_ == 0) wait_vmcnt<0>();                                           \
+    else if (STAGES == 3 || pend_ == 1) wait_vmcnt<(STAGES >= 3 ? G : 0)>();                  \
+    else wait_vmcnt<(STAGES >= 4 ? 2 * G : 0)>();                                             \
+    barrier_nofence();                                                                        \
+    if ((ks) + STAGES - 1 < nk) ART_ISSUE((ks) + STAGES - 1);                                 \
+  } while (0)
+
+    // Full 64-wide k-tiles of the base product: branch-free, fragments of step
+    // kk+1 are read while step kk multiplies.  (A separate loop keeps the
+    // accumulators in one register assignment across iterations.)
+    for (int ks = 0; ks < nk_full; ++ks) {
+      ART_STAGE_IN(ks);
+      const char *st = smem + (ks % STAGES) * STAGE_BYTES;
+      bf16x8 af0[TM], bf0[TN], af1[TM], bf1[TN];
+      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
+      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1);
+      mma_step<TM, TN>(acc, af0, bf0);
+      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
+      mma_step<TM, TN>(acc, af1, bf1);
+      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
+      mma_step<TM, TN>(acc, af0, bf0);
+      mma_step<TM, TN>(acc, af1, bf1);
+    }
+    // Tail: a partial base k-tile and the LoRA K-extension tiles.
+    for (int ks = nk_full; ks < nk; ++ks) {
+      ART_STAGE_IN(ks);
+      const char *st = smem + (ks % STAGES) * STAGE_BYTES;
+      const bool main = ks < nk_main;
+      const int kb = (main ? ks : ks - nk_main) * BK;
+      const int klim = main ? p.K : p.kt;
+      const int nkk = (klim - kb) >= BK ? BK / 16 : (klim - kb) / 16;
+      for (int kk = 0; kk < nkk; ++kk) {
         bf16x8 af[TM], bfv[TN];
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, kk, wm, wn, lrow, lk, af, bfv);
+        mma_step<TM, TN>(acc, af, bfv);
+      }
+    }
+#undef ART_STAGE_IN
+#undef ART_ISSUE
+    barrier_nofence();  // every wave is done reading the ring: reuse it for staging
+
+    // ------------------------------------------------------------ epilogue
+    // acc[i][j][v] is C[m][n] with m = wm*WTM + i*32 + lane%32 and
+    // n = wn*WTN + j*32 + 8*(v/4) + 4*(lane/32) + v%4 (tile-local).
+    uint2 *stg = (uint2 *)smem;  // staging tile, rows of BN bf16 in 8-byte units
+    constexpr int UPR = BN / 4;  // units per staging row
+    auto stage_unit = [&](int row, int unit, uint2 val) __attribute__((always_inline)) {
+      stg[row * UPR + (unit ^ (row & UMASK))] = val;
+    };
+    auto load_chunk = [&](int row, int chunk) __attribute__((always_inline)) -> U4 {
+      const uint2 lo = stg[row * UPR + ((2 * chunk) ^ (row & UMASK))];
+      const uint2 hi = stg[row * UPR + ((2 * chunk + 1) ^ (row & UMASK))];
+      return U4{lo.x, lo.y, hi.x, hi.y};
+    };
+
+    if (EPI == EPI_STORE) {
+      if (p.c_fp32) {
+        float *c = (float *)p.c;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-          const int r = wm * WTM + i * 32 + lrow;
-          af[i] = *(const bf16x8 *)&sA[st][r * BK + swz(r, kk * 2 + lk)];
-        }
+          const int m = m0 + wm * WTM + i * 32 + lrow;
+          if (m >= m_end) continue;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int r = wn * WTN + j * 32 + lrow;
-          bfv[j] = *(const bf16x8 *)&sB[st][r * BK + swz(r, kk * 2 + lk)];
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int n = nt * BN + wn * WTN + j * 32 + 8 * q + 4 * lk;
+              if (n < p.N) {
+                float4 v = make_float4(p.alpha * acc[i][j][4 * q], p.alpha * acc[i][j][4 * q + 1],
+                                       p.alpha * acc[i][j][4 * q + 2], p.alpha * acc[i][j][4 * q + 3]);
+                *(float4 *)(c + (int64_t)m * p.ldc + n) = v;
+              }
+            }
         }
+      } else {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfv[j], acc[i][j], 0, 0, 0);
-      }
-      if (ks + 1 < nk) lstore(st ^ 1);
-      __syncthreads();
-    }
-
-    // ------------------------------------------------------------ epilogue
-    // Accumulator element v of block (i, j) sits at row
-    // 8*(v/4) + 4*(lane/32) + v%4 and column lane%32 of the 32x32 block.
-    if (EPI == EPI_STORE) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int n = nt * BN + wn * WTN + j * 32 + lrow;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int m = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lk + (v & 3);
-            if (m < m_end && n < p.N) {
-              const float val = p.alpha * acc[i][j][v];
-              if (p.c_fp32) ((float *)p.c)[(int64_t)m * p.ldc + n] = val;
-              else ((bf16 *)p.c)[(int64_t)m * p.ldc + n] = (bf16)val;
+            for (int q = 0; q < 4; ++q) {
+              const int row = wm * WTM + i * 32 + lrow;
+              const int unit = (wn * WTN + j * 32) / 4 + 2 * q + lk;
+              stage_unit(row, unit,
+                         pack4(p.alpha * acc[i][j][4 * q], p.alpha * acc[i][j][4 * q + 1],
+                               p.alpha * acc[i][j][4 * q + 2], p.alpha * acc[i][j][4 * q + 3]));
             }
-          }
+        barrier_nofence();
+        bf16 *c = (bf16 *)p.c;
+        for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
+          const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
+          const int m = m0 + row, n = nt * BN + ch * 8;
+          if (m < m_end && n < p.N) *(U4 *)(c + (int64_t)m * p.ldc + n) = load_chunk(row, ch);
         }
+      }
     } else if (EPI == EPI_SWIGLU_FWD) {
       const int F = p.F;
+      // pass 1: y1 (gate and up, rounded to bf16) in logical column order
+      float hv[TM][TN / 2][16];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WTM + i * 32 + lrow;
+        const int m = m0 + row;
+        const float pr = p.prob[m < m_end ? m : m_end - 1];
 #pragma unroll
-        for (int jp = 0; jp < TN / 2; ++jp) {
-          const int f = nt * (BN / 2) + ((wn * TN) / 2 + jp) * 32 + lrow;
+        for (int jp = 0; jp < TN / 2; ++jp)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int m = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lk + (v & 3);
-            if (m < m_end && f < F) {
-              const bf16 gb = (bf16)(p.alpha * acc[i][2 * jp][v]);
-              const bf16 ub = (bf16)(p.alpha * acc[i][2 * jp + 1][v]);
-              const float g = (float)gb, u = (float)ub;
-              bf16 *yr = p.y1 + (int64_t)m * (2 * F);
-              yr[f] = gb;
-              yr[F + f] = ub;
-              p.h[(int64_t)m * F + f] = (bf16)(silu_f(g) * u * p.prob[m]);
+          for (int q = 0; q < 4; ++q) {
+            float gq[4], uq[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              gq[v] = (float)(bf16)acc[i][2 * jp][4 * q + v];
+              uq[v] = (float)(bf16)acc[i][2 * jp + 1][4 * q + v];
+              hv[i][jp][4 * q + v] = silu_f(gq[v]) * uq[v] * pr;
             }
+            const int ug = (wn * WTN + 2 * jp * 32) / 4 + 2 * q + lk;
+            stage_unit(row, ug, pack4(gq[0], gq[1], gq[2], gq[3]));
+            stage_unit(row, ug + 8, pack4(uq[0], uq[1], uq[2], uq[3]));
           }
-        }
-    } else {  // EPI_SWIGLU_BWD
-      const int F = p.F;
-      float rs[TM][16];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) rs[i][v] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int f = nt * BN + wn * WTN + j * 32 + lrow;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int m = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lk + (v & 3);
-            if (m < m_end && f < F) {
-              const float dh = p.alpha * acc[i][j][v];
-              const bf16 *yr = p.y1_in + (int64_t)m * (2 * F);
-              const float g = (float)yr[f], u = (float)yr[F + f];
-              const float pr = p.prob[m];
-              const float sg = sigmoid_f(g);
-              const float sl = g * sg;
-              const float dhp = dh * pr;
-              bf16 *dr = p.dy1 + (int64_t)m * (2 * F);
-              dr[f] = (bf16)(dhp * u * sg * (1.0f + g * (1.0f - sg)));
-              dr[F + f] = (bf16)(dhp * sl);
-              rs[i][v] += dh * sl * u;
-            }
-          }
-        }
-      // Sum over the 32 columns each half-wave holds, then over the WN waves.
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float s = rs[i][v];
-#pragma unroll
-          for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o, kWave);
-          rs[i][v] = s;
-        }
-      if (lrow == 0) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int v = 0; v < 16; ++v)
-            sRed[wn * BM + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lk + (v & 3)] = rs[i][v];
       }
-      __syncthreads();
-      for (int r = tid; r < BM; r += NT) {
+      barrier_nofence();
+      for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
+        const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
+        const int blk = ch >> 2;  // 32-column logical block
+        const int f = nt * (BN / 2) + (blk >> 1) * 32 + (ch & 3) * 8;
+        const int m = m0 + row;
+        if (m < m_end && f < F)
+          *(U4 *)(p.y1 + (int64_t)m * (2 * F) + ((blk & 1) ? F : 0) + f) = load_chunk(row, ch);
+      }
+      barrier_nofence();
+      // pass 2: h = silu(g) * u * p, tile-local columns 0 .. BN/2-1 (staging rows of BN/2)
+      constexpr int UPR2 = BN / 8;
+      constexpr int UMASK2 = (UPR2 >= 32) ? 31 : (UPR2 - 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int jp = 0; jp < TN / 2; ++jp)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int row = wm * WTM + i * 32 + lrow;
+            const int unit = ((wn * TN) / 2 + jp) * 8 + 2 * q + lk;
+            stg[row * UPR2 + (unit ^ (row & UMASK2))] =
+                pack4(hv[i][jp][4 * q], hv[i][jp][4 * q + 1], hv[i][jp][4 * q + 2], hv[i][jp][4 * q + 3]);
+          }
+      barrier_nofence();
+      for (int idx = tid; idx < BM * (BN / 16); idx += NT) {
+        const int row = idx / (BN / 16), ch = idx - row * (BN / 16);
+        const int f = nt * (BN / 2) + ch * 8;
+        const int m = m0 + row;
+        if (m < m_end && f < F) {
+          const uint2 lo = stg[row * UPR2 + ((2 * ch) ^ (row & UMASK2))];
+          const uint2 hi = stg[row * UPR2 + ((2 * ch + 1) ^ (row & UMASK2))];
+          *(U4 *)(p.h + (int64_t)m * F + f) = U4{lo.x, lo.y, hi.x, hi.y};
+        }
+      }
+    } else {  // EPI_SWIGLU_BWD: acc = dh over columns f of this tile
+      const int F = p.F;
+      uint2 du_pk[TM][TN][4];
+      float rs[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        rs[i] = 0.0f;
+        const int row = wm * WTM + i * 32 + lrow;
+        const int m = m0 + row;
+        const int mc = m < m_end ? m : m_end - 1;
+        const float pr = p.prob[mc];
+        const bf16 *yr = p.y1_in + (int64_t)mc * (2 * F);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            int f = nt * BN + wn * WTN + j * 32 + 8 * q + 4 * lk;
+            const bool fin = f < F;
+            f = fin ? f : 0;
+            const uint2 gr = *(const uint2 *)(yr + f);
+            const uint2 ur = *(const uint2 *)(yr + F + f);
+            const float g4[4] = {__uint_as_float(gr.x << 16), __uint_as_float(gr.x & 0xffff0000u),
+                                 __uint_as_float(gr.y << 16), __uint_as_float(gr.y & 0xffff0000u)};
+            const float u4[4] = {__uint_as_float(ur.x << 16), __uint_as_float(ur.x & 0xffff0000u),
+                                 __uint_as_float(ur.y << 16), __uint_as_float(ur.y & 0xffff0000u)};
+            float dg[4], du[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const float dh = p.alpha * acc[i][j][4 * q + v];
+              const float sg = sigmoid_f(g4[v]);
+              const float sl = g4[v] * sg;
+              const float dhp = dh * pr;
+              dg[v] = dhp * u4[v] * sg * (1.0f + g4[v] * (1.0f - sg));
+              du[v] = dhp * sl;
+              if (fin) rs[i] += dh * sl * u4[v];
+            }
+            du_pk[i][j][q] = pack4(du[0], du[1], du[2], du[3]);
+            stage_unit(row, (wn * WTN + j * 32) / 4 + 2 * q + lk, pack4(dg[0], dg[1], dg[2], dg[3]));
+          }
+        rs[i] += __shfl_xor(rs[i], 32, kWave);  // lanes l and l+32 share the row
+      }
+      if (lk == 0) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) sRed[wn * BM + wm * WTM + i * 32 + lrow] = rs[i];
+      }
+      barrier_nofence();
+      // dg -> dy1[:, f]
+      for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
+        const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
+        const int m = m0 + row, f = nt * BN + ch * 8;
+        if (m < m_end && f < F) *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + f) = load_chunk(row, ch);
+      }
+      // dp partial sums per 128-column group (independent of the tile width)
+      constexpr int WPG = 128 / WTN;                    // waves per 128-column group
+      constexpr int NGRP = (WN / WPG) > 0 ? (WN / WPG) : 1;
+      for (int idx = tid; idx < BM * NGRP; idx += NT) {
+        const int row = idx % BM, grp = idx / BM;
         float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WN; ++w) s += sRed[w * BM + r];
-        const int m = m0 + r;
-        if (m < m_end) p.dp_part[(int64_t)nt * p.M + m] = s;
+        for (int w = 0; w < WPG; ++w)
+          if (grp * WPG + w < WN) s += sRed[(grp * WPG + w) * BM + row];
+        const int m = m0 + row;
+        const int gcol = nt * BN + grp * 128;
+        if (m < m_end && gcol < F) p.dp_part[(int64_t)(gcol >> 7) * p.M + m] = s;
+      }
+      barrier_nofence();
+      // du -> dy1[:, F + f]
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            stage_unit(wm * WTM + i * 32 + lrow, (wn * WTN + j * 32) / 4 + 2 * q + lk, du_pk[i][j][q]);
+      barrier_nofence();
+      for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
+        const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
+        const int m = m0 + row, f = nt * BN + ch * 8;
+        if (m < m_end && f < F) *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + F + f) = load_chunk(row, ch);
       }
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
                      const char *what) {
   constexpr int bmi = BM == 32 ? 0 : BM == 64 ? 1 : BM == 128 ? 2 : 3;
   static_assert(BM == 32 || BM == 64 || BM == 128 || BM == 256, "BM must be 32<<b");
+  constexpr int NT = WM * WN * 64;
+  // Resident workgroups per CU for this instantiation (LDS / register bound).
+  static int occ = 0;
+  if (occ == 0) {
+    int o = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI>, NT, 0) != hipSuccess || o < 1)
+      o = 1;
+    occ = o;
+  }
   NTArgs p = a;
   p.seg_off = seg;
   p.tile_off = seg + (1 + bmi) * (a.E + 1);
   const int n_tiles = (a.N + BN - 1) / BN;
   const int64_t max_tiles = ((M + BM - 1) / BM + a.E) * (int64_t)n_tiles;
-  int64_t grid = (int64_t)device_cu_count() * 2;
+  int64_t grid = (int64_t)device_cu_count() * occ;
   if (grid > max_tiles) grid = max_tiles;
   if (grid >= 8) grid &= ~(int64_t)7;
   if (grid < 1) grid = 1;
-  gemm_nt_kernel<BM, BN, WM, WN, EPI><<<dim3((unsigned)grid), WM * WN * 64, 0, s>>>(p);
+  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI><<<dim3((unsigned)grid), NT, 0, s>>>(p);
   return check_launch(what);
+}
+
+// Macro-tile configurations of the large products, selectable with
+// ART_MOE_GEMM_TILE=<index> (the reference exposes ART_QUACK_* tile knobs):
+// 0: 128x128 (2x2 waves, 4 stages)  1: 128x256 (2x2, 3)  2: 256x128 (2x2, 3)
+// 3: 128x256 (2x4, 3)               4: 256x128 (4x2, 3)  5: 256x256 (2x4, 2)
+// 6: 256x256 (4x2, 2)               7: 256x256 (2x2, 2: 128x128 per wave)
+enum { kNumTileCfgs = 8 };
+// Defaults from a sweep of the C1 products on MI355X.
+enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 3 };
+
+template <int EPI>
+static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
+                      const char *what) {
+  switch (cfg) {
+    case 0: return launch_nt<128, 128, 2, 2, 4, EPI>(p, seg, M, s, what);
+    case 1: return launch_nt<128, 256, 2, 2, 3, EPI>(p, seg, M, s, what);
+    case 2: return launch_nt<256, 128, 2, 2, 3, EPI>(p, seg, M, s, what);
+    case 3: return launch_nt<128, 256, 2, 4, 3, EPI>(p, seg, M, s, what);
+    case 4: return launch_nt<256, 128, 4, 2, 3, EPI>(p, seg, M, s, what);
+    case 5: return launch_nt<256, 256, 2, 4, 2, EPI>(p, seg, M, s, what);
+    case 6: return launch_nt<256, 256, 4, 2, 2, EPI>(p, seg, M, s, what);
+    default: return launch_nt<256, 256, 2, 2, 2, EPI>(p, seg, M, s, what);
+  }
+}
+
+static int tile_cfg(int dflt) {
+  const char *v = getenv("ART_MOE_GEMM_TILE");
+  if (!v || !*v) return dflt;
+  const int c = atoi(v);
+  return (c >= 0 && c < kNumTileCfgs) ? c : dflt;
 }
 
 }  // namespace art
@@ -324,21 +583,26 @@ using namespace art;
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-// Shared argument checks: every 16-byte operand chunk must be aligned, so
-// base pointers are 16-byte aligned and leading dimensions multiples of 8.
+// Shared argument checks: operand rows are moved in 16-byte chunks and MFMA
+// steps are 16 wide, so base pointers are 16-byte aligned, leading dimensions
+// multiples of 8 and K a multiple of 16.
 static int check_common(const void *a, int64_t lda, const void *b, int64_t ldb,
                         const int32_t *seg, int32_t E, int64_t M, int32_t K, int32_t kt,
                         const void *tl, int64_t ldt, const void *l, int64_t ldl,
                         const char *who) {
   ART_REQUIRE(E >= 1 && E <= 1024, "%s: need 1 <= E <= 1024 (E=%d)", who, E);
   ART_REQUIRE(M >= 0 && M < INT32_MAX, "%s: M out of range", who);
-  ART_REQUIRE(K > 0 && K % 8 == 0, "%s: K must be a positive multiple of 8 (K=%d)", who, K);
+  ART_REQUIRE(K > 0 && K % 16 == 0, "%s: K must be a positive multiple of 16 (K=%d)", who, K);
   ART_REQUIRE(kt >= 0 && kt % 16 == 0, "%s: LoRA kt must be a multiple of 16 (kt=%d)", who, kt);
   ART_REQUIRE(a && b && seg, "%s: null pointer", who);
   ART_REQUIRE(lda >= K && lda % 8 == 0 && ldb >= K && ldb % 8 == 0,
               "%s: leading dimensions must be >= K and multiples of 8 (lda=%lld ldb=%lld)", who,
               (long long)lda, (long long)ldb);
   ART_REQUIRE(aligned16(a) && aligned16(b), "%s: A and B must be 16-byte aligned", who);
+  // The kernels address operand rows with 32-bit byte offsets.
+  const double k4g = 4294967296.0;
+  ART_REQUIRE((double)M * (double)lda * 2.0 < k4g && (double)M * (double)ldt * 2.0 < k4g,
+              "%s: A / Tl rows must span less than 4 GiB", who);
   if (kt) {
     ART_REQUIRE(tl && l, "%s: kt > 0 needs tl and l", who);
     ART_REQUIRE(ldt >= kt && ldt % 8 == 0 && ldl >= kt && ldl % 8 == 0,
@@ -357,7 +621,11 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   clear_error();
   int rc = check_common(a, lda, b, ldb, seg, E, M, K, kt, tl, ldt, l, ldl, "grouped_gemm");
   if (rc) return rc;
-  ART_REQUIRE(N > 0 && c, "grouped_gemm: need N > 0 and an output");
+  ART_REQUIRE(N > 0 && N % 8 == 0 && c, "grouped_gemm: need N a positive multiple of 8 and an output");
+  ART_REQUIRE(ldc >= N && ldc % 8 == 0 && aligned16(c),
+              "grouped_gemm: C needs ldc >= N, ldc %% 8 == 0 and 16-byte alignment");
+  ART_REQUIRE((double)N * (double)(ldb > ldl ? ldb : ldl) * 2.0 < 4294967296.0,
+              "grouped_gemm: one expert's B / L must span less than 4 GiB");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
@@ -366,9 +634,10 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   p.l = kt ? (const bf16 *)l : nullptr; p.ldl = ldl; p.l_es = l_estride; p.kt = kt;
   p.E = E; p.N = N; p.K = K; p.alpha = alpha; p.c = c; p.ldc = ldc; p.c_fp32 = c_fp32; p.M = M;
   hipStream_t s = as_stream(stream);
-  if (N <= 32) return launch_nt<128, 32, 4, 1, EPI_STORE>(p, seg, M, s, "grouped_gemm/n32");
-  if (N <= 64) return launch_nt<128, 64, 4, 1, EPI_STORE>(p, seg, M, s, "grouped_gemm/n64");
-  return launch_nt<128, 128, 2, 2, EPI_STORE>(p, seg, M, s, "grouped_gemm/n128");
+  if (N <= 32) return launch_nt<128, 32, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n32");
+  if (N <= 64) return launch_nt<128, 64, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n64");
+  if (N <= 128) return launch_nt<128, 128, 2, 2, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n128");
+  return launch_big<EPI_STORE>(tile_cfg(kTileStore), p, seg, M, s, "grouped_gemm");
 }
 
 extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
@@ -381,6 +650,7 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 64 == 0, "fc1_swiglu: F must be a positive multiple of 64 (F=%d)", F);
   ART_REQUIRE(row_prob && y1 && h, "fc1_swiglu: null pointer");
+  ART_REQUIRE(aligned16(y1) && aligned16(h), "fc1_swiglu: outputs must be 16-byte aligned");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
@@ -389,7 +659,8 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
   p.l = kt ? (const bf16 *)l1 : nullptr; p.ldl = kt; p.l_es = (int64_t)2 * F * kt; p.kt = kt;
   p.E = E; p.N = 2 * F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;
   p.y1 = (bf16 *)y1; p.h = (bf16 *)h; p.M = M;
-  return launch_nt<128, 128, 2, 2, EPI_SWIGLU_FWD>(p, seg, M, as_stream(stream), "fc1_swiglu");
+  return launch_big<EPI_SWIGLU_FWD>(tile_cfg(kTileSwigluFwd), p, seg, M, as_stream(stream),
+                                    "fc1_swiglu");
 }
 
 extern "C" int art_moe_dgrad_swiglu_parts(int32_t F) { return F > 0 ? (F + 127) / 128 : 0; }
@@ -405,6 +676,7 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 8 == 0, "fc2_dgrad_swiglu: F must be a positive multiple of 8 (F=%d)", F);
   ART_REQUIRE(y1 && row_prob && dy1 && dp_part, "fc2_dgrad_swiglu: null pointer");
+  ART_REQUIRE(aligned16(y1) && aligned16(dy1), "fc2_dgrad_swiglu: y1/dy1 must be 16-byte aligned");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
@@ -413,6 +685,6 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
   p.l = kt ? (const bf16 *)l2 : nullptr; p.ldl = kt; p.l_es = (int64_t)F * kt; p.kt = kt;
   p.E = E; p.N = F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;
   p.y1_in = (const bf16 *)y1; p.dy1 = (bf16 *)dy1; p.dp_part = dp_part; p.M = M;
-  return launch_nt<128, 128, 2, 2, EPI_SWIGLU_BWD>(p, seg, M, as_stream(stream),
-                                                   "fc2_dgrad_swiglu");
+  return launch_big<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwd), p, seg, M, as_stream(stream),
+                                    "fc2_dgrad_swiglu");
 }

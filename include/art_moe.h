@@ -143,7 +143,10 @@ int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
  * (ldb, b_estride); optional LoRA K-extension Tl bf16 [M][kt] (ldt) and
  * L bf16 [E][N][kt] (ldl, l_estride), kt % 16 == 0 (kt = 0: none).
  * C is bf16 (c_fp32 = 0) or fp32 (c_fp32 = 1) with leading dimension ldc.
- * K % 8 == 0.  Rows of C outside every segment are not written.
+ * K % 16 == 0, N % 8 == 0, leading dimensions multiples of 8, operands
+ * 16-byte aligned; rows are addressed with 32-bit byte offsets, so A rows
+ * (source rows below M), Tl and one expert's B / L each span < 4 GiB.
+ * Rows of C outside every segment are not written.
  * Replaces: TE GroupedLinear forward/dgrad (lora.py:1515-1521, 1559-1565),
  * QuACK varlen-M GEMMs (cute_grouped_lora_quack.py:257-298) and the
  * base + adapter add (lora.py:1529, 1571). */

@@ -56,7 +56,7 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     rc = lib.art_moe_grouped_gemm(null, 12, null, null, 12, 0, null, 0, null, 0, 0, 0, null, 4,
                                   16, 32, 12, 1.0, null, 32, 0, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
-    assert b"multiple of 8" in lib.art_moe_last_error()
+    assert b"multiple of 16" in lib.art_moe_last_error()
     rc = lib.art_moe_fc1_swiglu(null, 64, null, null, null, 0, null, 0, null, 4, 16, 100, 64,
                                 null, null, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG

@@ -49,7 +49,7 @@ CASES = [
     (8, 1000, 64, 768, False, 0, False),
     (16, 3000, 1536, 2048, True, 32, False),
     (128, 4096, 2048, 768, False, 16, False),
-    (4, 300, 200, 72, True, 16, False),
+    (4, 300, 200, 80, True, 16, False),
     (1, 777, 128, 2048, False, 0, True),
     (5, 64, 96, 64, False, 64, True),
 ]
@@ -91,7 +91,7 @@ def test_grouped_gemm_strided_output_and_operand(device):
     a = torch.randn(m, 3 * k, generator=g).to(torch.bfloat16)
     b = torch.randn(e, 48, k, generator=g).to(torch.bfloat16)
     seg = ops.segments_from_counts(counts, e, device)
-    out = torch.zeros(m, 100, dtype=torch.bfloat16, device=device)
+    out = torch.zeros(m, 104, dtype=torch.bfloat16, device=device)
     ops.grouped_gemm(a.to(device)[:, k:2 * k], b.to(device), seg, e, m=m, out=out[:, 40:88])
     ref = _ref_grouped(a[:, k:2 * k].float(), b, counts)
     assert rel(out[:, 40:88], ref) < 1e-2
@@ -189,3 +189,40 @@ def test_transpose(device):
     src = torch.randn(3, 70, 45).to(torch.bfloat16)
     got = ops.transposed(src.to(device), 2.0)
     assert torch.equal(got.cpu(), (src.float() * 2).transpose(1, 2).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("tile", range(8))
+def test_every_tile_config(device, tile, monkeypatch):
+    """All macro-tile configurations of the large kernels give the same products."""
+    ops = _ops()
+    monkeypatch.setenv("ART_MOE_GEMM_TILE", str(tile))
+    print(f"tile config {tile}", flush=True)
+    g = torch.Generator().manual_seed(100 + tile)
+    e, m, f, h, kt = 6, 1500, 384, 512, 32
+    counts = _counts(e, m, seed=tile)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(e, 2 * f, h, generator=g) * 0.03).to(torch.bfloat16)
+    tl = torch.randn(m, kt, generator=g).to(torch.bfloat16)
+    l1 = (torch.randn(e, 2 * f, kt, generator=g) * 0.05).to(torch.bfloat16)
+    prob = torch.rand(m, generator=g)
+    seg = ops.segments_from_counts(counts, e, device)
+    y1, hh = ops.fc1_swiglu(x.to(device), w1.to(device), seg, e, prob.to(device), m=m,
+                            tl=tl.to(device), l1=l1.to(device))
+    y1_ref = _ref_grouped(x.float(), w1, counts, tl, l1)
+    assert rel(y1, y1_ref) < 1e-2
+    gg, uu = y1.cpu().float().chunk(2, dim=1)
+    assert rel(hh, torch.nn.functional.silu(gg) * uu * prob[:, None]) < 1e-2
+    # plain product with N = 2F (large-kernel path)
+    c = ops.grouped_gemm(x.to(device), w1.to(device), seg, e, m=m, tl=tl.to(device), l=l1.to(device))
+    assert rel(c, y1_ref) < 1e-2
+    # FC2 data gradient + SwiGLU backward
+    w2t = (torch.randn(e, f, h, generator=g) * 0.03).to(torch.bfloat16)
+    dy1, dp_part = ops.fc2_dgrad_swiglu(x.to(device), w2t.to(device), seg, e, y1, prob.to(device),
+                                        m=m, tl=tl.to(device), l2=l1[:, :f].contiguous().to(device))
+    dh = _ref_grouped(x.float(), w2t, counts, tl, l1[:, :f])
+    y1f = y1.cpu().float().requires_grad_()
+    p = prob.clone().requires_grad_()
+    a_, b_ = y1f.chunk(2, dim=1)
+    (torch.nn.functional.silu(a_) * b_ * p[:, None]).backward(dh)
+    assert rel(dy1, y1f.grad) < 1e-2
+    assert rel(dp_part.sum(0), p.grad) < 1e-3
