@@ -153,6 +153,31 @@ def cpu_baseline(cfg, tokens: int, iters: int, seed: int = 0):
                        f"{dt:.2f} s/iter on {threads} threads")}
 
 
+def copy_calibration(mib: int, reps: int) -> None:
+    """Plain device copy of a known size, the reference point for scaling the
+    FETCH_SIZE / WRITE_SIZE counters of the profiled kernels."""
+    import torch
+    n = mib * 1024 * 1024 // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": n * 2, "reps": reps}))
+
+
+def measured_traffic(cfg_name: str):
+    """HBM bytes per launch of the dominant kernel from the committed profile
+    summary (two rocprofv3 --pmc passes), or None when not measured."""
+    path = REPO / "profiles" / f"fc1_swiglu_{cfg_name}_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -162,11 +187,16 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (profiler counter calibration)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, 3)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the expert-parallel sharding design is described in DESIGN.md). "
-              "Run with --gpus 1.", file=sys.stderr)
+              "(expert-parallel sharding is a design, not built). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     from art_amd.workloads import CONFIGS
@@ -207,7 +237,8 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd)",
                      "achieved": round(fc1_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(fc1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(fc1_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic(cfg.name),
                      "flops_per_launch": fc1_flops, "avg_launch_ms": round(fc1_ms, 4)},
         "gemm_mfma_frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "gemm_ms_per_step": round(gemm_ms, 4),
