@@ -113,6 +113,21 @@ __device__ __forceinline__ void issue_stage(char *st, int wave, const char *abas
     dma16((const bf16 *)(bbase + (boff[i] + sh)), st + A_BYTES + (wave * B_PW + i) * 1024);
 }
 
+// Weight row feeding tile-local B row r of column tile nt (clamped into range).
+// For the SwiGLU forward, logical 32-column blocks alternate gate / up rows of
+// the same columns so each lane ends up holding matching g and u.
+template <int EPI, int BN>
+__device__ __forceinline__ int b_source_row(int r, int nt, int N, int F) {
+  if (EPI == EPI_SWIGLU_FWD) {
+    const int blk = r >> 5;
+    int f = nt * (BN / 2) + (blk >> 1) * 32 + (r & 31);
+    f = f < F ? f : F - 1;
+    return ((blk & 1) ? F : 0) + f;
+  }
+  const int n = nt * BN + r;
+  return n < N ? n : N - 1;
+}
+
 // Stage DMA for a partial k-tile: a chunk past klim re-reads the row's last
 // chunk (those columns are never multiplied).  The logical chunk of block b's
 // slot is (lane & 7) ^ swz(8b + lane / 8).
@@ -215,10 +230,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // 32-bit byte offsets from wave-uniform bases (the host checks that every
     // operand spans less than 4 GiB).
     const char *abase = (const char *)p.a;
-    const char *tbase = (const char *)(p.t ? p.t : p.a);
     const char *bbase = (const char *)(p.b + (int64_t)e * p.b_es);
-    const char *lbase = p.l ? (const char *)(p.l + (int64_t)e * p.l_es) : bbase;
-    uint32_t aoff[A_PW], toff[A_PW], boff[B_PW], loff[B_PW];
+    uint32_t aoff[A_PW], boff[B_PW];
 #pragma unroll
     for (int i = 0; i < A_PW; ++i) {
       int m = m0 + (wave * A_PW + i) * 8 + drow;
@@ -226,26 +239,37 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       const uint32_t src = p.a_rows ? (uint32_t)p.a_rows[m] : (uint32_t)m;
       const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * A_PW + i) * 8 + drow));
       aoff[i] = (src * (uint32_t)p.lda + ch * 8) * 2u;
-      toff[i] = ((uint32_t)m * (uint32_t)p.ldt + ch * 8) * 2u;
     }
 #pragma unroll
     for (int i = 0; i < B_PW; ++i) {
       const int r = (wave * B_PW + i) * 8 + drow;
-      int n;
-      if (EPI == EPI_SWIGLU_FWD) {
-        // logical 32-column blocks alternate gate / up of the same columns
-        const int blk = r >> 5;
-        int f = nt * (BN / 2) + (blk >> 1) * 32 + (r & 31);
-        f = f < p.F ? f : p.F - 1;
-        n = ((blk & 1) ? p.F : 0) + f;
-      } else {
-        n = nt * BN + r;
-        n = n < p.N ? n : p.N - 1;
-      }
-      const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * B_PW + i) * 8 + drow));
+      const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
+      const uint32_t ch = (uint32_t)((lane & 7) ^ swz(r));
       boff[i] = ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
-      loff[i] = ((uint32_t)n * (uint32_t)p.ldl + ch * 8) * 2u;
     }
+
+    // LoRA K-extension stages: offsets into Tl (same rows, not gathered) and L,
+    // recomputed here so they do not occupy registers during the main loop.
+#define ART_ISSUE_LORA(ks)                                                                    \
+  do {                                                                                        \
+    uint32_t toff_[A_PW], loff_[B_PW];                                                        \
+    _Pragma("unroll") for (int i = 0; i < A_PW; ++i) {                                        \
+      int m = m0 + (wave * A_PW + i) * 8 + drow;                                              \
+      m = m < m_end ? m : m_end - 1;                                                          \
+      const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * A_PW + i) * 8 + drow));         \
+      toff_[i] = ((uint32_t)m * (uint32_t)p.ldt + ch * 8) * 2u;                               \
+    }                                                                                         \
+    _Pragma("unroll") for (int i = 0; i < B_PW; ++i) {                                        \
+      const int r = (wave * B_PW + i) * 8 + drow;                                             \
+      const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);                                   \
+      const uint32_t ch = (uint32_t)((lane & 7) ^ swz(r));                                    \
+      loff_[i] = ((uint32_t)n * (uint32_t)p.ldl + ch * 8) * 2u;                               \
+    }                                                                                         \
+    issue_stage_tail<A_PW, B_PW, A_BYTES>(smem + ((ks) % STAGES) * STAGE_BYTES, wave, lane,  \
+                                          (const char *)p.t,                                  \
+                                          (const char *)(p.l + (int64_t)e * p.l_es), toff_,   \
+                                          loff_, ((ks) - nk_main) * BK, p.kt);                \
+  } while (0)
 
 #define ART_ISSUE(ks)                                                                         \
   do {                                                                                        \
@@ -257,8 +281,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, abase, bbase, aoff, boff,        \
                                             (ks) * BK, p.K);                                  \
     else                                                                                      \
-      issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, tbase, lbase, toff, loff,        \
-                                            ((ks) - nk_main) * BK, p.kt);                     \
+      ART_ISSUE_LORA(ks);                                                                     \
   } while (0)
 
     f32x16 acc[TM][TN];
@@ -318,6 +341,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     }
 #undef ART_STAGE_IN
 #undef ART_ISSUE
+#undef ART_ISSUE_LORA
     barrier_nofence();  // every wave is done reading the ring: reuse it for staging
 
     // ------------------------------------------------------------ epilogue
@@ -521,8 +545,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
                      const char *what) {
-  constexpr int bmi = BM == 32 ? 0 : BM == 64 ? 1 : BM == 128 ? 2 : 3;
-  static_assert(BM == 32 || BM == 64 || BM == 128 || BM == 256, "BM must be 32<<b");
+  constexpr int bmi = BM / 64 - 1;  // segment-table row of this tile height
+  static_assert(BM == 64 || BM == 128 || BM == 192 || BM == 256, "BM must be 64, 128, 192 or 256");
   constexpr int NT = WM * WN * 64;
   // Resident workgroups per CU for this instantiation (LDS / register bound).
   static int occ = 0;
@@ -551,9 +575,10 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
 // 0: 128x128 (2x2 waves, 4 stages)  1: 128x256 (2x2, 3)  2: 256x128 (2x2, 3)
 // 3: 128x256 (2x4, 3)               4: 256x128 (4x2, 3)  5: 256x256 (2x4, 2)
 // 6: 256x256 (4x2, 2)               7: 256x256 (2x2, 2: 128x128 per wave)
-enum { kNumTileCfgs = 8 };
+// 8: 192x256 (2x4, 2)               9: 192x128 (2x2, 3)
+enum { kNumTileCfgs = 10 };
 // Defaults from a sweep of the C1 products on MI355X.
-enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 3 };
+enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 8 };
 
 template <int EPI>
 static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
@@ -566,6 +591,8 @@ static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, h
     case 4: return launch_nt<256, 128, 4, 2, 3, EPI>(p, seg, M, s, what);
     case 5: return launch_nt<256, 256, 2, 4, 2, EPI>(p, seg, M, s, what);
     case 6: return launch_nt<256, 256, 4, 2, 2, EPI>(p, seg, M, s, what);
+    case 8: return launch_nt<192, 256, 2, 4, 2, EPI>(p, seg, M, s, what);
+    case 9: return launch_nt<192, 128, 2, 2, 3, EPI>(p, seg, M, s, what);
     default: return launch_nt<256, 256, 2, 2, 2, EPI>(p, seg, M, s, what);
   }
 }

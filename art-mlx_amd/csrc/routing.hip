@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void plan_scan_kernel(
   if (threadIdx.x == 0) counts[e] = total;
 }
 
-// Segment table from counts: row offsets plus row-tile prefixes for BM = 32<<b.
+// Segment table from counts: row offsets plus row-tile prefixes for BM = 64*b.
 template <typename CT>
 __global__ __launch_bounds__(1024) void segments_kernel(const CT *__restrict__ counts, int E,
                                                         int32_t *__restrict__ seg) {
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(1024) void segments_kernel(const CT *__restrict__ c
     if (b == 0) {
       v = c;
     } else {
-      const int bm = 32 << (b - 1);
+      const int bm = 64 * b;  // row-tile heights 64, 128, 192, 256
       v = (c + bm - 1) / bm;
     }
     int total;

@@ -34,7 +34,7 @@
  *   device.  seg[0 .. E] are the row offsets of the E expert segments
  *   (exclusive prefix of tokens_per_expert); seg[(1+b)*(E+1) + e] for
  *   b = 0..ART_MOE_SEG_NBM-1 is the exclusive prefix over experts of
- *   ceil(count_e / BM_b) with BM_b = 32 << b (row-tile schedule of the grouped
+ *   ceil(count_e / BM_b) with BM_b = 64, 128, 192, 256 (row-tile schedules of the grouped
  *   GEMMs).  Build it with art_moe_dispatch_plan or art_moe_segments_from_counts.
  */
 #ifndef ART_MOE_H

@@ -26,7 +26,7 @@ def _seg_expect(counts, e):
     counts = np.asarray(counts, dtype=np.int64)
     rows = [np.concatenate([[0], np.cumsum(counts)])]
     for b in range(4):
-        bm = 32 << b
+        bm = 64 * (b + 1)
         rows.append(np.concatenate([[0], np.cumsum((counts + bm - 1) // bm)]))
     return np.concatenate(rows)
 
