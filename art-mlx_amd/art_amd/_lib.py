@@ -22,6 +22,10 @@ ART_MOE_ERR_INVALID_ARG = -1
 ART_MOE_ERR_UNSUPPORTED = -2
 ART_MOE_ERR_HIP = -3
 SEG_NBM = 4
+PACK_MAX = 8
+WGRAD_STORE = 0
+WGRAD_ACCUMULATE = 1
+WGRAD_STORE_BF16 = 2
 
 
 def seg_len(num_experts: int) -> int:
@@ -56,7 +60,18 @@ SIGNATURES = {
     "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I32, _I32, _F, _P,
                                      _I64, _I64, _I64, _I32, _P]),
     "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
+    "art_moe_pack": (_I32, [_P, _I32, _P]),
 }
+
+
+class PackDesc(ctypes.Structure):
+    """art_moe_pack_desc (include/art_moe.h)."""
+    _fields_ = [("src", _P), ("dst", _P),
+                ("s_es", _I64), ("s_rs", _I64), ("s_cs", _I64),
+                ("d_es", _I64), ("d_rs", _I64),
+                ("E", _I32), ("R", _I32), ("C", _I32),
+                ("src_r", _I32), ("src_c", _I32),
+                ("scale", _F)]
 
 
 class ArtMoeError(RuntimeError):

@@ -117,19 +117,20 @@ def padded_rank(rank: int) -> int:
 def proj_operand(a_ts, ranks_padded) -> torch.Tensor:
     """[E, sum(RP), in]: the A factors transposed and stacked along padded rank."""
     e, d_in = a_ts[0].shape[0], a_ts[0].shape[1]
-    out = a_ts[0].new_zeros((e, sum(ranks_padded), d_in))
-    off = 0
+    out = a_ts[0].new_empty((e, sum(ranks_padded), d_in))
+    items, off = [], 0
     for a_t, rp in zip(a_ts, ranks_padded):
-        ops.transpose_into(a_t, out[:, off:off + a_t.shape[-1], :])
+        items.append((out[:, off:off + rp], a_t.transpose(1, 2), 1.0))
         off += rp
+    ops.pack(*items)
     return out
 
 
 def apply_operand(b_t: torch.Tensor, rp: int, scale: float = 1.0) -> torch.Tensor:
     """[E, out, RP]: B transposed (optionally scaled), rank zero-padded."""
-    e, r, d_out = b_t.shape
-    out = b_t.new_zeros((e, d_out, rp))
-    ops.transpose_into(b_t, out[:, :, :r], scale)
+    e, _r, d_out = b_t.shape
+    out = b_t.new_empty((e, d_out, rp))
+    ops.pack((out, b_t.transpose(1, 2), scale))
     return out
 
 
@@ -137,17 +138,29 @@ def pad_rank_last(a_t: torch.Tensor, rp: int) -> torch.Tensor:
     """[E, in, RP] copy of A_T with zero rank padding (A_T itself if already padded)."""
     if a_t.shape[-1] == rp and a_t.is_contiguous():
         return a_t
-    out = a_t.new_zeros((*a_t.shape[:-1], rp))
-    out[..., : a_t.shape[-1]] = a_t
+    out = a_t.new_empty((*a_t.shape[:-1], rp))
+    ops.pack((out, a_t, 1.0))
     return out
 
 
 def pad_rank_mid(b_t: torch.Tensor, rp: int) -> torch.Tensor:
-    """[E, RP, out] copy of B_T with zero rank padding."""
+    """[E, RP, out] copy of B_T with zero rank padding (B_T itself if already padded)."""
     if b_t.shape[1] == rp and b_t.is_contiguous():
         return b_t
-    out = b_t.new_zeros((b_t.shape[0], rp, b_t.shape[2]))
-    out[:, : b_t.shape[1]] = b_t
+    out = b_t.new_empty((b_t.shape[0], rp, b_t.shape[2]))
+    ops.pack((out, b_t, 1.0))
+    return out
+
+
+def concat_rank_last(a_ts, ranks_padded) -> torch.Tensor:
+    """[E, in, sum(RP)]: the A factors side by side, each rank zero-padded."""
+    e, d_in = a_ts[0].shape[0], a_ts[0].shape[1]
+    out = a_ts[0].new_empty((e, d_in, sum(ranks_padded)))
+    items, off = [], 0
+    for a_t, rp in zip(a_ts, ranks_padded):
+        items.append((out[:, :, off:off + rp], a_t, 1.0))
+        off += rp
+    ops.pack(*items)
     return out
 
 
@@ -178,9 +191,10 @@ class _HipGroupedLoraFn(torch.autograd.Function):
         rp, scale, m = ctx.rp, ctx.scale, x.shape[0]
         grad_tmp = ops.grouped_gemm(grad_out, pad_rank_mid(b_t, rp), seg, e, m=m, alpha=scale)
         grad_x = ops.grouped_gemm(grad_tmp, pad_rank_last(a_t, rp), seg, e, m=m)
-        grad_a = ops.grouped_wgrad(x, grad_tmp, seg, e)
-        grad_b = ops.grouped_wgrad(grad_out, tmp, seg, e, alpha=scale, transpose_out=True)
-        return (grad_x, grad_a[:, :, :r].to(a_t.dtype), grad_b[:, :r, :].to(b_t.dtype), None, None)
+        grad_a = ops.grouped_wgrad(x, grad_tmp, seg, e, out_dtype=a_t.dtype)
+        grad_b = ops.grouped_wgrad(grad_out, tmp, seg, e, alpha=scale, transpose_out=True,
+                                   out_dtype=b_t.dtype)
+        return (grad_x, grad_a[:, :, :r], grad_b[:, :r, :], None, None)
 
 
 class _HipGroupedLoraDualFn(torch.autograd.Function):
@@ -220,19 +234,15 @@ class _HipGroupedLoraDualFn(torch.autograd.Function):
                          out=grad_tmp[:, :rpg])
         ops.grouped_gemm(grad_out[:, fg:], pad_rank_mid(up_b_t, rpu), seg, e, m=m, alpha=su,
                          out=grad_tmp[:, rpg:])
-        a_cat = torch.cat((pad_rank_last(gate_a_t, rpg), pad_rank_last(up_a_t, rpu)), dim=-1)
+        a_cat = concat_rank_last([gate_a_t, up_a_t], [rpg, rpu])
         grad_x = ops.grouped_gemm(grad_tmp, a_cat, seg, e, m=m)
-        grad_a = ops.grouped_wgrad(x, grad_tmp, seg, e)
+        grad_a = ops.grouped_wgrad(x, grad_tmp, seg, e, out_dtype=x.dtype)
         grad_bg = ops.grouped_wgrad(grad_out[:, :fg], tmp[:, :rpg], seg, e, alpha=sg,
-                                    transpose_out=True)
+                                    transpose_out=True, out_dtype=x.dtype)
         grad_bu = ops.grouped_wgrad(grad_out[:, fg:], tmp[:, rpg:], seg, e, alpha=su,
-                                    transpose_out=True)
-        return (grad_x,
-                grad_a[:, :, :rg].to(gate_a_t.dtype),
-                grad_bg[:, :rg, :].to(gate_b_t.dtype),
-                grad_a[:, :, rpg:rpg + ru].to(up_a_t.dtype),
-                grad_bu[:, :ru, :].to(up_b_t.dtype),
-                None, None, None)
+                                    transpose_out=True, out_dtype=x.dtype)
+        return (grad_x, grad_a[:, :, :rg], grad_bg[:, :rg, :], grad_a[:, :, rpg:rpg + ru],
+                grad_bu[:, :ru, :], None, None, None)
 
 
 @torch.compiler.disable

@@ -36,7 +36,7 @@ from typing import Any
 import torch
 
 from .. import ops
-from .kernels.grouped_lora_hip import apply_operand, pad_rank_last, pad_rank_mid, padded_rank, proj_operand
+from .kernels.grouped_lora_hip import padded_rank
 
 
 @dataclass
@@ -109,16 +109,25 @@ class _MoELoRALayerFn(torch.autograd.Function):
         rows = plan.row_token
         rg, ru, rd = a_g.shape[-1], a_u.shape[-1], a_d.shape[-1]
         rpg, rpu, rpd = padded_rank(rg), padded_rank(ru), padded_rank(rd)
-        # LoRA operand layouts (tiny; rebuilt every call since the factors train)
-        a1p = proj_operand([a_g, a_u], [rpg, rpu])                 # [E, RPg+RPu, H]
-        l1 = a_g.new_zeros((e, 2 * f, rpg + rpu))                 # [E, 2F, RPg+RPu]
-        ops.transpose_into(b_g, l1[:, :f, :rg], sg)
-        ops.transpose_into(b_u, l1[:, f:, rpg:rpg + ru], su)
+        # LoRA operand layouts, rebuilt every call since the factors train: one
+        # launch writes the transposed, rank-padded and scaled copies
+        a1p = x.new_empty((e, rpg + rpu, h_dim))   # [A_g | A_u]^T
+        l1 = x.new_empty((e, 2 * f, rpg + rpu))    # [[s_g B_g^T, 0], [0, s_u B_u^T]]
+        a2p = x.new_empty((e, rpd, f))             # A_d^T
+        l2 = x.new_empty((e, h_dim, rpd))          # s_d B_d^T
+        ops.pack((a1p[:, :rpg], a_g.transpose(1, 2), 1.0),
+                 (a1p[:, rpg:], a_u.transpose(1, 2), 1.0),
+                 (l1[:, :f, :rpg], b_g.transpose(1, 2), sg),
+                 (l1[:, :f, rpg:], None, 0.0),
+                 (l1[:, f:, :rpg], None, 0.0),
+                 (l1[:, f:, rpg:], b_u.transpose(1, 2), su),
+                 (a2p, a_d.transpose(1, 2), 1.0),
+                 (l2, b_d.transpose(1, 2), sd))
         t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
         y1, h = ops.fc1_swiglu(x, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
                                tl=t1, l1=l1)
-        t2 = ops.grouped_gemm(h, proj_operand([a_d], [rpd]), plan.seg, e, m=m)
-        y2 = ops.grouped_gemm(h, base.w2, plan.seg, e, m=m, tl=t2, l=apply_operand(b_d, rpd, sd))
+        t2 = ops.grouped_gemm(h, a2p, plan.seg, e, m=m)
+        y2 = ops.grouped_gemm(h, base.w2, plan.seg, e, m=m, tl=t2, l=l2)
         y = ops.combine(y2, plan.dest, t)
         ctx.save_for_backward(x, idx, w, plan.dest, rows, plan.row_prob, plan.seg, t1, y1, h, t2,
                               a_g, b_g, a_u, b_u, a_d, b_d)
@@ -138,17 +147,27 @@ class _MoELoRALayerFn(torch.autograd.Function):
         t = x.shape[0]
         m = t * k
         dy = dy.contiguous()
+        h_dim = base.hidden
+        # backward operand layouts in one launch: B_d and A_d rank-padded, the
+        # block-diagonal [[s_g B_g, 0], [0, s_u B_u]] (g1 = [s_g dg B_g^T | s_u du B_u^T]
+        # as one product, dy1 read once) and [A_g | A_u]
+        bdp = b_d if rd == rpd and b_d.is_contiguous() else dy.new_empty((e, rpd, h_dim))
+        adp = a_d if rd == rpd and a_d.is_contiguous() else dy.new_empty((e, f, rpd))
+        gb = dy.new_empty((e, rpg + rpu, 2 * f))
+        a1cat = dy.new_empty((e, h_dim, rpg + rpu))
+        items = [(gb[:, :rpg, :f], b_g, sg), (gb[:, :rpg, f:], None, 0.0),
+                 (gb[:, rpg:, :f], None, 0.0), (gb[:, rpg:, f:], b_u, su),
+                 (a1cat[:, :, :rpg], a_g, 1.0), (a1cat[:, :, rpg:], a_u, 1.0)]
+        if bdp is not b_d:
+            items.append((bdp, b_d, 1.0))
+        if adp is not a_d:
+            items.append((adp, a_d, 1.0))
+        ops.pack(*items)
         # FC2 data gradient with the SwiGLU backward in its epilogue
-        g2 = ops.grouped_gemm(dy, pad_rank_mid(b_d, rpd), seg, e, m=m, a_rows=rows, alpha=sd)
+        g2 = ops.grouped_gemm(dy, bdp, seg, e, m=m, a_rows=rows, alpha=sd)
         dy1, dp_part = ops.fc2_dgrad_swiglu(dy, base.w2t, seg, e, y1, row_prob, m=m, a_rows=rows,
-                                            tl=g2, l2=pad_rank_last(a_d, rpd))
-        # g1 = [s_g dg B_g^T | s_u du B_u^T] as one product (dy1 read once) with
-        # the block-diagonal operand [[s_g B_g, 0], [0, s_u B_u]]
-        gb = b_g.new_zeros((e, rpg + rpu, 2 * f))
-        gb[:, :rg, :f] = b_g * sg
-        gb[:, rpg:rpg + ru, f:] = b_u * su
+                                            tl=g2, l2=adp)
         g1 = ops.grouped_gemm(dy1, gb, seg, e, m=m)
-        a1cat = torch.cat((pad_rank_last(a_g, rpg), pad_rank_last(a_u, rpu)), dim=-1)
         dx_perm = ops.grouped_gemm(dy1, base.w1t, seg, e, m=m, tl=g1, l=a1cat)
         # router: softmax backward over the k selected logits
         dl, dlogits = ops.router_backward(dp_part, dest, w, idx, e,
@@ -157,12 +176,16 @@ class _MoELoRALayerFn(torch.autograd.Function):
             dx = ops.combine(dx_perm, dest, t, dl=dl, idx=idx, w_r=base.w_r)
         else:
             dx = ops.combine(dx_perm, dest, t)
-        # LoRA weight gradients (fp32 accumulation, returned in parameter dtype)
-        da1 = ops.grouped_wgrad(x, g1, seg, e, l_rows=rows)                          # [E,H,RP1]
-        dbg = ops.grouped_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, alpha=sg, transpose_out=True)
-        dbu = ops.grouped_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, alpha=su, transpose_out=True)
-        dad = ops.grouped_wgrad(h, g2, seg, e)                                        # [E,F,RPd]
-        dbd = ops.grouped_wgrad(dy, t2, seg, e, alpha=sd, l_rows=rows, transpose_out=True)
+        # LoRA weight gradients: fp32 accumulation, rounded once to the parameter dtype
+        od = torch.bfloat16 if a_g.dtype == torch.bfloat16 else torch.float32
+        da1 = ops.grouped_wgrad(x, g1, seg, e, l_rows=rows, out_dtype=od)             # [E,H,RP1]
+        dbg = ops.grouped_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, alpha=sg, transpose_out=True,
+                                out_dtype=od)
+        dbu = ops.grouped_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, alpha=su, transpose_out=True,
+                                out_dtype=od)
+        dad = ops.grouped_wgrad(h, g2, seg, e, out_dtype=od)                           # [E,F,RPd]
+        dbd = ops.grouped_wgrad(dy, t2, seg, e, alpha=sd, l_rows=rows, transpose_out=True,
+                                out_dtype=od)
         return (dx, dlogits, None,
                 da1[:, :, :rg].to(a_g.dtype), dbg[:, :rg].to(b_g.dtype),
                 da1[:, :, rpg:rpg + ru].to(a_u.dtype), dbu[:, :ru].to(b_u.dtype),

@@ -6,6 +6,7 @@ current stream.  No function synchronizes with the host.
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -241,21 +242,31 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
 def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_experts: int, *,
                   alpha: float = 1.0, l_rows: torch.Tensor | None = None,
                   r_rows: torch.Tensor | None = None, transpose_out: bool = False,
-                  out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
-    """out[e] = alpha * Lm_e^T @ R_e (fp32 [E,P,Q]; [E,Q,P] with transpose_out)."""
+                  out: torch.Tensor | None = None, accumulate: bool = False,
+                  out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """out[e] = alpha * Lm_e^T @ R_e ([E,P,Q]; [E,Q,P] with transpose_out).
+
+    fp32 accumulation; the output is fp32 or, with ``out_dtype=torch.bfloat16``,
+    the fp32 sum rounded once to bf16.  ``accumulate`` adds to an fp32 ``out``.
+    """
     _cuda(lm, r, seg, l_rows, r_rows, out)
     p, q = lm.shape[-1], r.shape[-1]
     if out is None:
         shape = (num_experts, q, p) if transpose_out else (num_experts, p, q)
-        out = torch.empty(shape, dtype=torch.float32, device=lm.device)
-    _need(out.dtype == torch.float32, "wgrad output must be fp32")
+        out = torch.empty(shape, dtype=out_dtype, device=lm.device)
+    _need(out.dtype in (torch.float32, torch.bfloat16), "wgrad output must be fp32 or bf16")
+    _need(not (accumulate and out.dtype != torch.float32), "wgrad accumulates into fp32 only")
+    if accumulate:
+        mode = _lib.WGRAD_ACCUMULATE
+    else:
+        mode = _lib.WGRAD_STORE_BF16 if out.dtype == torch.bfloat16 else _lib.WGRAD_STORE
     if transpose_out:
         o_es, o_ps, o_qs = out.stride(0), out.stride(2), out.stride(1)
     else:
         o_es, o_ps, o_qs = out.stride(0), out.stride(1), out.stride(2)
     call("art_moe_grouped_wgrad", ptr(lm), _rowmajor(lm, "Lm"), ptr(l_rows), ptr(r), _rowmajor(r, "R"),
          ptr(r_rows), ptr(seg), num_experts, p, q, float(alpha), ptr(out), o_es, o_ps, o_qs,
-         int(accumulate), stream_ptr(lm.device))
+         mode, stream_ptr(lm.device))
     return out
 
 
@@ -275,3 +286,35 @@ def transposed(src: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
     e, r, c = src.shape
     dst = torch.empty((e, c, r), dtype=src.dtype, device=src.device)
     return transpose_into(src, dst, scale)
+
+
+def pack(*items) -> None:
+    """Batched strided copies in one launch (at most 8 per call).
+
+    Each item is ``(dst, src, scale)``: ``dst`` an [E, R, C] bf16 view with a
+    contiguous last dimension, ``src`` an [E, Rs, Cs] bf16 view with any
+    strides (a ``.transpose(1, 2)`` view reads transposed) or None.  Writes
+    ``dst[e, r, c] = scale * src[e, r, c]`` where ``r < Rs`` and ``c < Cs``,
+    zero elsewhere.
+    """
+    _need(len(items) <= _lib.PACK_MAX, f"pack takes at most {_lib.PACK_MAX} copies")
+    descs = (_lib.PackDesc * max(len(items), 1))()
+    dev = None
+    for i, (dst, src, scale) in enumerate(items):
+        _cuda(dst, src)
+        _need(dst.dim() == 3 and dst.dtype == torch.bfloat16 and dst.stride(2) == 1,
+              "pack destination must be an [E, R, C] bf16 view with contiguous last dim")
+        e, rr, cc = dst.shape
+        d = descs[i]
+        d.dst, d.d_es, d.d_rs = dst.data_ptr(), dst.stride(0), dst.stride(1)
+        d.E, d.R, d.C, d.scale = e, rr, cc, float(scale)
+        if src is not None:
+            _need(src.dim() == 3 and src.dtype == torch.bfloat16 and src.shape[0] == e,
+                  "pack source must be an [E, Rs, Cs] bf16 view")
+            _need(src.shape[1] <= rr and src.shape[2] <= cc, "pack source larger than destination")
+            d.src = src.data_ptr()
+            d.s_es, d.s_rs, d.s_cs = src.stride(0), src.stride(1), src.stride(2)
+            d.src_r, d.src_c = src.shape[1], src.shape[2]
+        dev = dst.device
+    if items:
+        call("art_moe_pack", ctypes.cast(descs, ctypes.c_void_p), len(items), stream_ptr(dev))

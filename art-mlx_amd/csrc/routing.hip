@@ -390,6 +390,104 @@ __global__ __launch_bounds__(256) void transpose_kernel(const bf16 *__restrict__
   }
 }
 
+// ---------------------------------------------------------------- pack
+struct PackArgs {
+  art_moe_pack_desc d[ART_MOE_PACK_MAX];
+  int32_t tile_start[ART_MOE_PACK_MAX + 1];  // prefix of tiles over descriptors
+  int32_t tc_log2[ART_MOE_PACK_MAX];         // tile = (4096 >> tc_log2) x (1 << tc_log2)
+  int32_t vec_read[ART_MOE_PACK_MAX];        // 16-byte source loads allowed
+  int32_t vec_write[ART_MOE_PACK_MAX];       // 16-byte destination stores allowed
+  int n;
+};
+
+constexpr int kPackTile = 4096;  // elements per workgroup tile
+
+// Tile width: the destination's row length rounded up to a power of two in
+// [16, 256], capped at 64 when the block is also tall (square-ish copies),
+// so that rank-sized dimensions (16..64) fill whole tiles.
+static int pack_tc_log2(int R, int C) {
+  int l = 4;
+  while (l < 8 && (1 << l) < C) ++l;
+  if (R >= 64 && l > 6) l = 6;
+  return l;
+}
+
+// One workgroup per tile of one expert; each thread moves two runs of 8
+// elements.  Source runs follow the source's fast index (the one with stride
+// 1 when there is one: coalesced for plain and transposed reads alike), are
+// parked in LDS as fp32 (row pitch TC+1), and leave as 8-element runs along
+// destination rows.  Runs are 16-byte accesses where the host found strides
+// and alignment to allow it and the run is whole; element accesses otherwise.
+__global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
+  __shared__ float tile[kPackTile + 256];
+  const int b = blockIdx.x;
+  int k = 0;
+  while (k + 1 < a.n && a.tile_start[k + 1] <= b) ++k;
+  const art_moe_pack_desc &d = a.d[k];
+  const int tcl = a.tc_log2[k];
+  const int TC = 1 << tcl, TR = kPackTile >> tcl, pitch = TC + 1;
+  const int lb = b - a.tile_start[k];
+  const int tcn = (d.C + TC - 1) / TC, per_e = ((d.R + TR - 1) / TR) * tcn;
+  const int e = lb / per_e, rem = lb - e * per_e;
+  const int r0 = (rem / tcn) * TR, c0 = (rem % tcn) * TC;
+  const bool cfast = d.s_cs == 1;
+  const int64_t fstride = cfast ? d.s_cs : d.s_rs;
+  const int f8l = (cfast ? tcl : 12 - tcl) - 3;  // log2(runs per fast line)
+  const int fast_lim = cfast ? d.src_c : d.src_r, slow_lim = cfast ? d.src_r : d.src_c;
+  const bool vr = a.vec_read[k] != 0, vw = a.vec_write[k] != 0;
+  const bf16 *src = (const bf16 *)d.src + (int64_t)e * d.s_es;
+
+  float v[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int u = j * 256 + (int)threadIdx.x;
+    const int f0 = (u & ((1 << f8l) - 1)) * 8, sl = u >> f8l;
+    const int rb = r0 + (cfast ? sl : f0), cb = c0 + (cfast ? f0 : sl);
+    const int fa = cfast ? cb : rb, sa = cfast ? rb : cb;
+    const bf16 *p = src + (int64_t)rb * d.s_rs + (int64_t)cb * d.s_cs;
+    if (sa < slow_lim && vr && fa + 8 <= fast_lim) {
+      unpack8(*(const U4 *)p, v[j]);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[j][t] *= d.scale;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        v[j][t] = (sa < slow_lim && fa + t < fast_lim) ? d.scale * (float)p[t * fstride] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int u = j * 256 + (int)threadIdx.x;
+    const int f0 = (u & ((1 << f8l) - 1)) * 8, sl = u >> f8l;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int rr = cfast ? sl : f0 + t, cc = cfast ? f0 + t : sl;
+      tile[rr * pitch + cc] = v[j][t];
+    }
+  }
+  __syncthreads();
+  bf16 *dst = (bf16 *)d.dst + (int64_t)e * d.d_es;
+  const int c8l = tcl - 3;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int u = j * 256 + (int)threadIdx.x;
+    const int cc0 = (u & ((1 << c8l) - 1)) * 8, rr = u >> c8l;
+    const int r = r0 + rr, c = c0 + cc0;
+    if (r >= d.R) continue;
+    float w[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) w[t] = tile[rr * pitch + cc0 + t];
+    bf16 *q = dst + (int64_t)r * d.d_rs + c;
+    if (vw && c + 8 <= d.C) {
+      *(U4 *)q = pack8(w);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (c + t < d.C) q[t] = (bf16)w[t];
+    }
+  }
+}
+
 }  // namespace art
 
 using namespace art;
@@ -537,4 +635,38 @@ extern "C" int art_moe_transpose(const void *src, int32_t E, int32_t R, int32_t 
   transpose_kernel<<<grid, 256, 0, as_stream(stream)>>>((const bf16 *)src, R, C, s_es, s_ld,
                                                         (bf16 *)dst, d_es, d_ld, scale);
   return check_launch("transpose");
+}
+
+extern "C" int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *stream) {
+  clear_error();
+  ART_REQUIRE(n >= 0 && n <= ART_MOE_PACK_MAX, "pack: need 0 <= n <= %d (n=%d)", ART_MOE_PACK_MAX, n);
+  if (n == 0) return ART_MOE_OK;
+  ART_REQUIRE(descs, "pack: null descriptor array");
+  PackArgs a{};
+  a.n = n;
+  a.tile_start[0] = 0;
+  int64_t tiles = 0;
+  for (int k = 0; k < n; ++k) {
+    const art_moe_pack_desc &d = descs[k];
+    ART_REQUIRE(d.E >= 0 && d.R >= 0 && d.C >= 0 && d.src_r >= 0 && d.src_c >= 0,
+                "pack: negative extent in descriptor %d", k);
+    ART_REQUIRE(d.dst || (int64_t)d.E * d.R * d.C == 0, "pack: null destination in descriptor %d", k);
+    ART_REQUIRE(d.src || d.src_r == 0 || d.src_c == 0 || (int64_t)d.E * d.R * d.C == 0,
+                "pack: null source in descriptor %d", k);
+    a.d[k] = d;
+    const int tcl = pack_tc_log2(d.R, d.C);
+    const int TC = 1 << tcl, TR = kPackTile >> tcl;
+    a.tc_log2[k] = tcl;
+    const bool cfast = d.s_cs == 1;
+    const int64_t slow_stride = cfast ? d.s_rs : d.s_cs;
+    a.vec_read[k] = ((cfast || d.s_rs == 1) && ((uintptr_t)d.src & 15) == 0 && d.s_es % 8 == 0 &&
+                     slow_stride % 8 == 0) ? 1 : 0;
+    a.vec_write[k] = (((uintptr_t)d.dst & 15) == 0 && d.d_es % 8 == 0 && d.d_rs % 8 == 0) ? 1 : 0;
+    tiles += (int64_t)d.E * ((d.R + TR - 1) / TR) * ((d.C + TC - 1) / TC);
+    ART_REQUIRE(tiles < (int64_t)1 << 31, "pack: too many tiles");
+    a.tile_start[k + 1] = (int32_t)tiles;
+  }
+  if (tiles == 0) return ART_MOE_OK;
+  pack_kernel<<<dim3((unsigned)tiles), 256, 0, as_stream(stream)>>>(a);
+  return check_launch("pack");
 }

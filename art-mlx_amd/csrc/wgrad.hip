@@ -30,9 +30,9 @@ struct WArgs {
   const int32_t *seg;
   int E, P, Q;
   float alpha;
-  float *out;
+  void *out;
   int64_t o_es, o_sp, o_sq;
-  int accumulate;
+  int mode;  // ART_MOE_WGRAD_STORE / _ACCUMULATE / _STORE_BF16
 };
 
 template <int BP, int BQ>
@@ -117,9 +117,14 @@ __global__ __launch_bounds__(256) void wgrad_tn_kernel(const WArgs a) {
         const int pp = p0 + wave * (BP / 4) + i * 16 + g4 * 4 + v;
         const int qq = q0 + j * 16 + l16;
         if (pp < a.P && qq < a.Q) {
-          float *o = a.out + (int64_t)e * a.o_es + (int64_t)pp * a.o_sp + (int64_t)qq * a.o_sq;
+          const int64_t off = (int64_t)e * a.o_es + (int64_t)pp * a.o_sp + (int64_t)qq * a.o_sq;
           const float val = a.alpha * acc[i][j][v];
-          *o = a.accumulate ? *o + val : val;
+          if (a.mode == ART_MOE_WGRAD_STORE_BF16) {
+            ((bf16 *)a.out)[off] = (bf16)val;
+          } else {
+            float *o = (float *)a.out + off;
+            *o = a.mode == ART_MOE_WGRAD_ACCUMULATE ? *o + val : val;
+          }
         }
       }
 }
@@ -138,21 +143,24 @@ using namespace art;
 extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
                                      const void *r, int64_t ldr, const int32_t *r_rows,
                                      const int32_t *seg, int32_t E, int32_t P, int32_t Q,
-                                     float alpha, float *out, int64_t o_es, int64_t o_ps,
-                                     int64_t o_qs, int32_t accumulate, void *stream) {
+                                     float alpha, void *out, int64_t o_es, int64_t o_ps,
+                                     int64_t o_qs, int32_t mode, void *stream) {
   clear_error();
   ART_REQUIRE(E >= 1 && E <= 65535, "grouped_wgrad: need 1 <= E <= 65535 (E=%d)", E);
   ART_REQUIRE(P > 0 && Q > 0 && P % 8 == 0 && Q % 8 == 0,
               "grouped_wgrad: P and Q must be positive multiples of 8 (P=%d Q=%d)", P, Q);
   ART_REQUIRE(ldl % 8 == 0 && ldr % 8 == 0, "grouped_wgrad: row strides must be multiples of 8");
   ART_REQUIRE(lm && r && seg && out, "grouped_wgrad: null pointer");
+  ART_REQUIRE(mode == ART_MOE_WGRAD_STORE || mode == ART_MOE_WGRAD_ACCUMULATE ||
+                  mode == ART_MOE_WGRAD_STORE_BF16,
+              "grouped_wgrad: unknown mode %d", mode);
   ART_REQUIRE(((uintptr_t)lm & 15) == 0 && ((uintptr_t)r & 15) == 0,
               "grouped_wgrad: operands must be 16-byte aligned");
   WArgs a{};
   a.l = (const bf16 *)lm; a.ldl = ldl; a.l_rows = l_rows;
   a.r = (const bf16 *)r; a.ldr = ldr; a.r_rows = r_rows;
   a.seg = seg; a.E = E; a.P = P; a.Q = Q; a.alpha = alpha;
-  a.out = out; a.o_es = o_es; a.o_sp = o_ps; a.o_sq = o_qs; a.accumulate = accumulate;
+  a.out = out; a.o_es = o_es; a.o_sp = o_ps; a.o_sq = o_qs; a.mode = mode;
   hipStream_t s = as_stream(stream);
   if (Q <= 16) return launch_wgrad<128, 16>(a, s);
   if (Q <= 32) return launch_wgrad<128, 32>(a, s);

@@ -36,7 +36,7 @@ NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
 # ops whose time counts as GEMM (MFMA roofline) vs bandwidth-bound (HBM roofline)
 GEMM_OPS = ("grouped_gemm", "fc1_swiglu", "fc2_dgrad_swiglu", "grouped_wgrad")
 HBM_OPS = ("router_topk", "router_replay", "dispatch_plan", "combine", "router_backward",
-           "permute", "transpose_into", "segments_from_counts")
+           "permute", "transpose_into", "segments_from_counts", "pack")
 
 
 class OpTimer:

@@ -191,21 +191,27 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
                              const void *y1, const float *row_prob, void *dy1,
                              float *dp_part, void *stream);
 
+#define ART_MOE_WGRAD_STORE 0
+#define ART_MOE_WGRAD_ACCUMULATE 1
+#define ART_MOE_WGRAD_STORE_BF16 2
+
 /* Segmented "TN" product (LoRA weight gradients, fp32 accumulation):
  *   out[e*o_es + p*o_ps + q*o_qs] (+)=
  *       alpha * sum_{m in segment e} Lm[lrow(m), p] * R[rrow(m), q]
  * Lm bf16 rows (ldl) with lrow(m) = l_rows ? l_rows[m] : m, likewise R;
  * P, Q, ldl, ldr multiples of 8, operands 16-byte aligned.
- * out is fp32; (o_ps, o_qs) = (Q, 1) writes [E][P][Q], (1, P) writes the
- * transpose [E][Q][P].  accumulate != 0 adds to out.
+ * (o_ps, o_qs) = (Q, 1) writes [E][P][Q], (1, P) writes the transpose
+ * [E][Q][P].  mode: ART_MOE_WGRAD_STORE writes fp32 out, _ACCUMULATE adds to
+ * fp32 out, _STORE_BF16 writes bf16 out (one rounding of the fp32 sum: the
+ * parameter-dtype gradient the reference returns).
  * Experts with no rows get zeros (or keep out when accumulating).
  * Replaces: QuACK varlen-K GEMMs for grad_A / grad_B
  * (cute_grouped_lora_quack.py:301-334, 411-431, 585-616). */
 int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
                           const void *r, int64_t ldr, const int32_t *r_rows,
                           const int32_t *seg, int32_t E, int32_t P, int32_t Q,
-                          float alpha, float *out, int64_t o_es,
-                          int64_t o_ps, int64_t o_qs, int32_t accumulate,
+                          float alpha, void *out, int64_t o_es,
+                          int64_t o_ps, int64_t o_qs, int32_t mode,
                           void *stream);
 
 /* Batched strided transpose with scale:
@@ -215,6 +221,29 @@ int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
 int art_moe_transpose(const void *src, int32_t E, int32_t R, int32_t C,
                       int64_t s_es, int64_t s_ld, void *dst, int64_t d_es,
                       int64_t d_ld, float scale, void *stream);
+
+/* One strided copy of art_moe_pack: for e < E, r < R, c < C
+ *   dst[e*d_es + r*d_rs + c] = bf16(scale * src[e*s_es + r*s_rs + c*s_cs])
+ *                              if r < src_r and c < src_c, else 0.
+ * Strides are in elements (bf16).  A transpose is a swap of s_rs and s_cs. */
+typedef struct {
+  const void *src;
+  void *dst;
+  int64_t s_es, s_rs, s_cs;
+  int64_t d_es, d_rs;
+  int32_t E, R, C;
+  int32_t src_r, src_c;
+  float scale;
+} art_moe_pack_desc;
+
+#define ART_MOE_PACK_MAX 8
+
+/* Up to ART_MOE_PACK_MAX strided copies in one launch: builds the padded,
+ * transposed and scaled LoRA operand layouts of the grouped products (zero
+ * padding of the rank dimension included) from the A_T / B_T parameters.
+ * Replaces the rank padding / permute / cat copies of
+ * cute_grouped_lora_quack.py:205-224, 350-353, 465-468. */
+int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *stream);
 
 #ifdef __cplusplus
 }

@@ -184,6 +184,98 @@ def test_grouped_wgrad(device, e, m, p, q, gather, transpose):
             assert torch.count_nonzero(got[i]) == 0
 
 
+def test_grouped_wgrad_bf16_and_accumulate_modes(device):
+    """bf16 output is the fp32 result rounded once; accumulate adds to fp32 out."""
+    ops = _ops()
+    e, m, p, q = 8, 1500, 320, 32
+    g = torch.Generator().manual_seed(77)
+    counts = _counts(e, m, seed=5)
+    lm = torch.randn(m, p, generator=g).to(torch.bfloat16).to(device)
+    r = torch.randn(m, q, generator=g).to(torch.bfloat16).to(device)
+    seg = ops.segments_from_counts(counts, e, device)
+    for tr in (False, True):
+        f32 = ops.grouped_wgrad(lm, r, seg, e, alpha=0.5, transpose_out=tr)
+        b16 = ops.grouped_wgrad(lm, r, seg, e, alpha=0.5, transpose_out=tr, out_dtype=torch.bfloat16)
+        assert b16.dtype == torch.bfloat16
+        assert torch.equal(b16.cpu(), f32.cpu().to(torch.bfloat16))
+        base = torch.randn(f32.shape, generator=g).to(device)
+        acc = base.clone()
+        ops.grouped_wgrad(lm, r, seg, e, alpha=0.5, transpose_out=tr, out=acc, accumulate=True)
+        assert torch.equal(acc.cpu(), (base + f32).cpu())
+    with pytest.raises(ValueError):
+        ops.grouped_wgrad(lm, r, seg, e, out=b16, accumulate=True)
+
+
+def test_pack_layouts(device):
+    """Strided, transposed, scaled, zero-padded copies in one launch vs torch."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(11)
+    a = torch.randn(5, 70, 12, generator=g).to(torch.bfloat16)   # A_T-like [E, in, r]
+    b = torch.randn(5, 12, 130, generator=g).to(torch.bfloat16)  # B_T-like [E, r, out]
+    ad, bd = a.to(device), b.to(device)
+    p1 = torch.full((5, 32, 70), 7.0, dtype=torch.bfloat16, device=device)
+    p2 = torch.full((5, 130, 16), 7.0, dtype=torch.bfloat16, device=device)
+    blk = torch.full((5, 32, 260), 7.0, dtype=torch.bfloat16, device=device)
+    sqs = torch.randn(5, 90, 100, generator=g).to(torch.bfloat16)  # square-ish transposed copy
+    sq = torch.empty((5, 100, 90), dtype=torch.bfloat16, device=device)
+    ops.pack((p1[:, :16], ad.transpose(1, 2), 1.0), (p1[:, 16:], None, 0.0),
+             (p2, bd.transpose(1, 2), 0.75),
+             (blk[:, :16, :130], bd, 2.0), (blk[:, :16, 130:], None, 0.0),
+             (blk[:, 16:, :130], None, 0.0), (blk[:, 16:, 130:], bd[:, :7], -1.0),
+             (sq, sqs.to(device).transpose(1, 2), 3.0))
+    torch.cuda.synchronize()
+    assert torch.equal(sq.cpu(), (sqs.float().transpose(1, 2) * 3.0).to(torch.bfloat16))
+
+    def r16(t):
+        return t.to(torch.bfloat16)
+    e1 = torch.zeros(5, 32, 70)
+    e1[:, :12] = a.float().transpose(1, 2)
+    e2 = torch.zeros(5, 130, 16)
+    e2[:, :, :12] = b.float().transpose(1, 2) * 0.75
+    e3 = torch.zeros(5, 32, 260)
+    e3[:, :12, :130] = b.float() * 2.0
+    e3[:, 16:23, 130:] = -b.float()[:, :7]
+    assert torch.equal(p1.cpu(), r16(e1))
+    assert torch.equal(p2.cpu(), r16(e2))
+    assert torch.equal(blk.cpu(), r16(e3))
+    with pytest.raises(ValueError):
+        ops.pack(*[(p2, None, 0.0)] * 9)
+
+
+@pytest.mark.parametrize("e,h,f,r", [(4, 256, 192, 16), (3, 512, 96, 12), (2, 136, 64, 64)])
+def test_pack_layer_operands(device, e, h, f, r):
+    """The layer's operand layouts (16-byte paths where aligned) vs torch."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(e * h + r)
+    rp = (r + 15) // 16 * 16
+    ag, bg = (torch.randn(e, h, r, generator=g).to(torch.bfloat16),
+              torch.randn(e, r, f, generator=g).to(torch.bfloat16))
+    a1p = torch.empty((e, 2 * rp, h), dtype=torch.bfloat16, device=device)
+    l1 = torch.empty((e, 2 * f, 2 * rp), dtype=torch.bfloat16, device=device)
+    gb = torch.empty((e, 2 * rp, 2 * f), dtype=torch.bfloat16, device=device)
+    a1c = torch.empty((e, h, 2 * rp), dtype=torch.bfloat16, device=device)
+    agd, bgd = ag.to(device), bg.to(device)
+    ops.pack((a1p[:, :rp], agd.transpose(1, 2), 1.0), (a1p[:, rp:], agd.transpose(1, 2), 0.5),
+             (l1[:, :f, :rp], bgd.transpose(1, 2), 2.0), (l1[:, :f, rp:], None, 0.0),
+             (l1[:, f:, :rp], None, 0.0), (l1[:, f:, rp:], bgd.transpose(1, 2), -1.0),
+             (gb[:, :rp, :f], bgd, 3.0), (a1c[:, :, rp:], agd, 1.0))
+    ops.pack((gb[:, :rp, f:], None, 0.0), (gb[:, rp:, :f], None, 0.0), (gb[:, rp:, f:], bgd, 1.0),
+             (a1c[:, :, :rp], agd, 1.0))
+    torch.cuda.synchronize()
+    af, bf = ag.float(), bg.float()
+    e1 = torch.zeros(e, 2 * rp, h)
+    e1[:, :r], e1[:, rp:rp + r] = af.transpose(1, 2), 0.5 * af.transpose(1, 2)
+    e2 = torch.zeros(e, 2 * f, 2 * rp)
+    e2[:, :f, :r], e2[:, f:, rp:rp + r] = 2.0 * bf.transpose(1, 2), -bf.transpose(1, 2)
+    e3 = torch.zeros(e, 2 * rp, 2 * f)
+    e3[:, :r, :f], e3[:, rp:rp + r, f:] = 3.0 * bf, bf
+    e4 = torch.zeros(e, h, 2 * rp)
+    e4[:, :, :r], e4[:, :, rp:rp + r] = af, af
+    for got, exp in ((a1p, e1), (l1, e2), (gb, e3), (a1c, e4)):
+        assert torch.equal(got.cpu(), exp.to(torch.bfloat16))
+        assert not torch.signbit(got.cpu()[exp == 0]).any()  # zero padding is +0
+
+
 def test_transpose(device):
     ops = _ops()
     src = torch.randn(3, 70, 45).to(torch.bfloat16)
