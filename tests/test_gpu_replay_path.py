@@ -1,0 +1,112 @@
+"""Routing replay end to end on the GPU: a bundle written and read in the
+reference's on-disk format, the controller staging per-micro targets to the
+device, and the HIP router / fused layer consuming them.
+
+Bar: replayed indices, counts and routing maps bit-exact against the bundle
+rows of the micro's token uids; router weights and their logit gradients
+against the CPU oracle (fp32, 1e-6).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import routing as R
+
+pytestmark = pytest.mark.gpu
+KEY = "chunk_00.layer_0000.mlp.router"
+
+
+class _Chunk(torch.nn.Module):
+    def __init__(self, router):
+        super().__init__()
+        mlp = torch.nn.Module()
+        mlp.router = router
+        layer = torch.nn.Module()
+        layer.mlp = mlp
+        self.decoder = torch.nn.Module()
+        self.decoder.layers = torch.nn.ModuleList([layer])
+
+
+def _bundle(rows, num_experts, tmp_path):
+    from art_amd.megatron import routing_replay as RR
+    idx = torch.as_tensor(rows, dtype=torch.int32)
+    call = RR.RouterCallRoute(expert_indices=idx, expert_mask=torch.ones_like(idx, dtype=torch.bool),
+                              num_experts=num_experts, sample_index=0)
+    b = RR.MoeRoutingReplayBundle(
+        topology=RR.ParallelTopology(tp=1, ep=1), num_steps=1, max_topk=idx.shape[1],
+        router_keys=[KEY],
+        steps={0: RR.StepRoutes(routers={KEY: RR.StepRouterRoutes(calls={0: call})},
+                                global_token_uids=torch.arange(idx.shape[0], dtype=torch.int64))})
+    b.to_dir(tmp_path)
+    return RR.MoeRoutingReplayBundle.from_dir(tmp_path)
+
+
+def test_controller_targets_drive_hip_router_and_layer(device, tmp_path):
+    from art_amd import ops
+    from art_amd.megatron import routing_replay as RR
+    from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
+    from art_amd.megatron.router import TopKRouter
+    from art_amd.workloads import zipf_targets
+
+    t, h, e, k, f, r = 2048, 256, 128, 8, 128, 16
+    rows = zipf_targets(t, e, k, seed=3)          # Zipf(1.2) ids, some experts empty
+    bundle = _bundle(rows, e, tmp_path)
+    router = TopKRouter(h, e, k, moe_enable_routing_replay=True, device=device)
+    ctl = RR.MoeRoutingReplayController(bundle=bundle, strict=True, device=device)
+    ctl.install_router_patches([_Chunk(router)])
+    ctl.set_step(step_index=0, sample_index=[0])
+    ctl.begin_micro(0, 0)
+    g = torch.Generator().manual_seed(5)
+    uids = torch.randperm(t, generator=g)[:1500]   # the micro's tokens, out of order
+    ctl.set_local_input_token_uids(uids)
+    x = torch.randn(1500, h, generator=g).to(torch.bfloat16).to(device)
+    logits = router.gating(x)
+    probs, rmap = router.routing(logits)
+    want = rows[uids]
+    assert torch.equal(router.router_replay.target_topk_idx.cpu(), want)
+    exp_map = torch.zeros((1500, e), dtype=torch.bool)
+    exp_map[torch.arange(1500).unsqueeze(1), want] = True
+    assert torch.equal(rmap.cpu(), exp_map)
+    assert int(router.last_status.item()) == 0
+    _, exp_w = R.replay(logits.detach().cpu().numpy(), want.numpy())
+    np.testing.assert_allclose(probs.gather(1, want.to(device)).detach().cpu().numpy(), exp_w,
+                               rtol=2e-6, atol=1e-7)
+    # the fused layer consumes the same staged target
+    target = router.router_replay.target_topk_idx
+    wts = [torch.randn(e, 2 * f, h, generator=g) * 0.02, torch.randn(e, h, f, generator=g) * 0.02]
+    base = FrozenExperts.build(router.weight, *(w.to(torch.bfloat16).to(device) for w in wts))
+    lora = [(torch.randn(s, generator=g) * 0.01).to(torch.bfloat16).to(device)
+            for s in [(e, h, r), (e, r, f), (e, h, r), (e, r, f), (e, f, r), (e, r, h)]]
+    y, idx, counts, status = moe_lora_layer(x, base, *lora, k=k, scales=(2.0, 2.0, 2.0),
+                                            target=target)
+    assert torch.equal(idx.cpu().long(), want)
+    assert counts.cpu().tolist() == torch.bincount(want.reshape(-1), minlength=e).tolist()
+    assert int(status.item()) == 0
+    ctl.finalize_step()
+    ctl.remove_router_patches()
+
+
+def test_topk_router_module_matches_oracle(device):
+    from art_amd.megatron.router import TopKRouter
+    t, h, e, k = 1000, 512, 64, 6
+    router = TopKRouter(h, e, k, device=device)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16).to(device)
+    logits = router.gating(x).detach().requires_grad_()
+    exp_logits = x.float().cpu() @ router.weight.float().cpu().T
+    torch.testing.assert_close(logits.detach().cpu(), exp_logits, rtol=1e-5, atol=1e-5)
+    probs, rmap = router.routing(logits)
+    exp_idx, exp_w = R.topk_softmax(logits.detach().cpu().numpy(), k)
+    idx = torch.from_numpy(exp_idx).long()
+    exp_map = torch.zeros((t, e), dtype=torch.bool)
+    exp_map[torch.arange(t).unsqueeze(1), idx] = True
+    assert torch.equal(rmap.cpu(), exp_map)
+    np.testing.assert_allclose(probs.detach().cpu().gather(1, idx).numpy(), exp_w, rtol=2e-6,
+                               atol=1e-7)
+    # softmax-over-selected backward vs torch autograd on the CPU
+    gout = torch.randn(t, e, generator=g)
+    (probs * gout.to(device)).sum().backward()
+    lc = logits.detach().cpu().requires_grad_()
+    sel = torch.softmax(lc.gather(1, idx), dim=1)
+    (sel * gout.gather(1, idx)).sum().backward()
+    torch.testing.assert_close(logits.grad.cpu(), lc.grad, rtol=1e-5, atol=1e-6)
