@@ -22,7 +22,7 @@ ART_MOE_ERR_INVALID_ARG = -1
 ART_MOE_ERR_UNSUPPORTED = -2
 ART_MOE_ERR_HIP = -3
 SEG_NBM = 4
-PACK_MAX = 8
+PACK_MAX = 16
 WGRAD_STORE = 0
 WGRAD_ACCUMULATE = 1
 WGRAD_STORE_BF16 = 2
@@ -49,7 +49,7 @@ SIGNATURES = {
     "art_moe_dispatch_plan": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "art_moe_segments_from_counts": (_I32, [_P, _I32, _P, _P]),
     "art_moe_permute": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P]),
-    "art_moe_combine": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _P]),
+    "art_moe_combine": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _P]),
     "art_moe_grouped_gemm": (_I32, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I32,
                                     _P, _I32, _I64, _I32, _I32, _F, _P, _I64, _I32, _P]),
     "art_moe_fc1_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _I32, _P, _I32, _I64, _I32,
@@ -58,9 +58,11 @@ SIGNATURES = {
     "art_moe_fc2_dgrad_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _I32, _P, _I32, _I64,
                                         _I32, _I32, _P, _P, _P, _P, _P]),
     "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I32, _I32, _F, _P,
-                                     _I64, _I64, _I64, _I32, _P]),
+                                     _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P]),
     "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
     "art_moe_pack": (_I32, [_P, _I32, _P]),
+    "art_moe_router_lora_apply": (_I32, [_P, _I64, _I32, _P, _I32, _F, _P, _P, _P]),
+    "art_moe_router_lora_grad": (_I32, [_P, _P, _I64, _I32, _P, _I32, _I32, _F, _P, _P, _P]),
 }
 
 

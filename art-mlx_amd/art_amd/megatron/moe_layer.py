@@ -79,26 +79,117 @@ def _single_segment(num_rows: int, device) -> torch.Tensor:
     return ops.segments_from_counts(counts, 1, device)
 
 
-def router_logits(x: torch.Tensor, w_r: torch.Tensor) -> torch.Tensor:
+def router_logits(x: torch.Tensor, w_r: torch.Tensor, seg: torch.Tensor | None = None,
+                  router_lora: tuple[torch.Tensor, torch.Tensor, float] | None = None
+                  ) -> torch.Tensor:
     """logits = x.float() @ W_r.float().T on bf16 MFMA with fp32 accumulation
-    (products of bf16 values are exact in fp32)."""
+    (products of bf16 values are exact in fp32), plus s (x A_r) B_r in fp32
+    when ``router_lora = (A_r [H,r], B_r [r,E], s)`` is given."""
     t = x.shape[0]
-    seg = _single_segment(t, x.device)
-    return ops.grouped_gemm(x, w_r.unsqueeze(0), seg, 1, m=t, out_fp32=True)
+    seg = _single_segment(t, x.device) if seg is None else seg
+    logits = ops.grouped_gemm(x, w_r.unsqueeze(0), seg, 1, m=t, out_fp32=True)
+    if router_lora is not None:
+        a_r, b_r, s = router_lora
+        rp = padded_rank(a_r.shape[1])
+        arp = x.new_empty((1, rp, x.shape[1]))
+        brp = x.new_empty((1, rp, w_r.shape[0]))
+        ops.pack((arp, a_r.t().unsqueeze(0), 1.0), (brp, b_r.unsqueeze(0), 1.0))
+        t_r = ops.grouped_gemm(x, arp, seg, 1, m=t, out_fp32=True)
+        ops.router_lora_apply(t_r, brp[0], logits, s)
+    return logits
+
+
+def _rank_of(p: torch.Tensor, transpose_out: bool) -> int:
+    return p.shape[-2] if transpose_out else p.shape[-1]
+
+
+def _as3(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dim() == 3 else t.unsqueeze(0)
+
+
+def _land_wgrad(lm, r, seg, e, targets, *, alpha=1.0, l_rows=None, transpose_out=False,
+                fuse_main_grad=False):
+    """Weight gradients of LoRA factors from one segmented TN product.
+
+    ``targets`` lists ``(param, q0)``: the param's gradient is the product's
+    columns ``[q0, q0 + rank)`` (rows with ``transpose_out``); a param without
+    an expert dimension is expert 0 of a one-segment product.  With
+    ``fuse_main_grad`` and an fp32 ``param.main_grad`` on every target, the
+    gradient is accumulated there (megatron's gradient-accumulation fusion:
+    ``grad_added_to_main_grad`` is set and autograd gets None); otherwise the
+    fp32 sums are rounded once to the parameter dtype and returned.
+    """
+    q = r.shape[-1]
+    kw = dict(alpha=alpha, l_rows=l_rows, transpose_out=transpose_out)
+    ranks = [_rank_of(p, transpose_out) for p, _ in targets]
+    mgs = [getattr(p, "main_grad", None) for p, _ in targets]
+    if fuse_main_grad and all(mg is not None and mg.dtype == torch.float32 and mg.shape == p.shape
+                              for mg, (p, _) in zip(mgs, targets)):
+        q0s = [q0 for _, q0 in targets]
+        exact = (len(targets) == 1 and q0s[0] == 0 and ranks[0] == q) or (
+            len(targets) == 2 and q0s[0] == 0 and ranks[0] == q0s[1] and q0s[1] + ranks[1] == q)
+        if exact:
+            ops.grouped_wgrad(lm, r, seg, e, out=_as3(mgs[0]), accumulate=True,
+                              out2=_as3(mgs[1]) if len(targets) == 2 else None,
+                              q_split=q0s[1] if len(targets) == 2 else 0, **kw)
+        else:   # padded ranks: land through an fp32 scratch product
+            tmp = ops.grouped_wgrad(lm, r, seg, e, **kw)
+            for mg, q0, rk in zip(mgs, q0s, ranks):
+                _as3(mg).add_(tmp[:, q0:q0 + rk] if transpose_out else tmp[:, :, q0:q0 + rk])
+        for p, _ in targets:
+            p.grad_added_to_main_grad = True
+        return [None] * len(targets)
+    od = torch.bfloat16 if targets[0][0].dtype == torch.bfloat16 else torch.float32
+    full = ops.grouped_wgrad(lm, r, seg, e, out_dtype=od, **kw)
+    grads = []
+    for (p, q0), rk in zip(targets, ranks):
+        g = full[:, q0:q0 + rk] if transpose_out else full[:, :, q0:q0 + rk]
+        grads.append((g if p.dim() == 3 else g[0]).to(p.dtype))
+    return grads
 
 
 class _MoELoRALayerFn(torch.autograd.Function):
 
     @staticmethod
-    def forward(ctx, x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, base: FrozenExperts,
-                k: int, scales: tuple[float, float, float]):
+    def forward(ctx, x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r,
+                base: FrozenExperts, k: int, scales: tuple[float, float, float], scale_r: float,
+                fuse_main_grad: bool):
         e, h_dim, f = base.num_experts, base.hidden, base.ffn
         sg, su, sd = scales
         x = x.contiguous()
         t = x.shape[0]
         logits_supplied = logits is not None
+        seg1 = _single_segment(t, x.device)
+        rg, ru, rd = a_g.shape[-1], a_u.shape[-1], a_d.shape[-1]
+        rpg, rpu, rpd = padded_rank(rg), padded_rank(ru), padded_rank(rd)
+        rr = a_r.shape[-1] if a_r is not None else 0
+        rpr = padded_rank(rr) if rr else 0
+        # LoRA operand layouts, rebuilt every call since the factors train: one
+        # launch writes the transposed, rank-padded and scaled copies
+        a1p = x.new_empty((e, rpg + rpu, h_dim))   # [A_g | A_u]^T
+        l1 = x.new_empty((e, 2 * f, rpg + rpu))    # [[s_g B_g^T, 0], [0, s_u B_u^T]]
+        a2p = x.new_empty((e, rpd, f))             # A_d^T
+        l2 = x.new_empty((e, h_dim, rpd))          # s_d B_d^T
+        items = [(a1p[:, :rpg], a_g.transpose(1, 2), 1.0),
+                 (a1p[:, rpg:], a_u.transpose(1, 2), 1.0),
+                 (l1[:, :f, :rpg], b_g.transpose(1, 2), sg),
+                 (l1[:, :f, rpg:], None, 0.0),
+                 (l1[:, f:, :rpg], None, 0.0),
+                 (l1[:, f:, rpg:], b_u.transpose(1, 2), su),
+                 (a2p, a_d.transpose(1, 2), 1.0),
+                 (l2, b_d.transpose(1, 2), sd)]
+        arp = brp = None
+        if rr:
+            arp = x.new_empty((1, rpr, h_dim))     # A_r^T
+            brp = x.new_empty((1, rpr, e))         # B_r, rank zero-padded
+            items += [(arp, a_r.t().unsqueeze(0), 1.0), (brp, b_r.unsqueeze(0), 1.0)]
+        ops.pack(*items)
+        t_rb = None
         if not logits_supplied:
-            logits = router_logits(x, base.w_r)
+            logits = router_logits(x, base.w_r, seg1)
+            if rr:   # router LoRA term in fp32: logits += s_r (x A_r) B_r
+                t_r = ops.grouped_gemm(x, arp, seg1, 1, m=t, out_fp32=True)
+                t_rb = ops.router_lora_apply(t_r, brp[0], logits, scale_r, want_bf16=True)
         if target is None:
             idx, w = ops.router_topk(logits, k)
             status = None
@@ -107,22 +198,6 @@ class _MoELoRALayerFn(torch.autograd.Function):
         plan = ops.dispatch_plan(idx, w, e, status=status)
         m = t * k
         rows = plan.row_token
-        rg, ru, rd = a_g.shape[-1], a_u.shape[-1], a_d.shape[-1]
-        rpg, rpu, rpd = padded_rank(rg), padded_rank(ru), padded_rank(rd)
-        # LoRA operand layouts, rebuilt every call since the factors train: one
-        # launch writes the transposed, rank-padded and scaled copies
-        a1p = x.new_empty((e, rpg + rpu, h_dim))   # [A_g | A_u]^T
-        l1 = x.new_empty((e, 2 * f, rpg + rpu))    # [[s_g B_g^T, 0], [0, s_u B_u^T]]
-        a2p = x.new_empty((e, rpd, f))             # A_d^T
-        l2 = x.new_empty((e, h_dim, rpd))          # s_d B_d^T
-        ops.pack((a1p[:, :rpg], a_g.transpose(1, 2), 1.0),
-                 (a1p[:, rpg:], a_u.transpose(1, 2), 1.0),
-                 (l1[:, :f, :rpg], b_g.transpose(1, 2), sg),
-                 (l1[:, :f, rpg:], None, 0.0),
-                 (l1[:, f:, :rpg], None, 0.0),
-                 (l1[:, f:, rpg:], b_u.transpose(1, 2), su),
-                 (a2p, a_d.transpose(1, 2), 1.0),
-                 (l2, b_d.transpose(1, 2), sd))
         t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
         y1, h = ops.fc1_swiglu(x, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
                                tl=t1, l1=l1)
@@ -130,19 +205,20 @@ class _MoELoRALayerFn(torch.autograd.Function):
         y2 = ops.grouped_gemm(h, base.w2, plan.seg, e, m=m, tl=t2, l=l2)
         y = ops.combine(y2, plan.dest, t)
         ctx.save_for_backward(x, idx, w, plan.dest, rows, plan.row_prob, plan.seg, t1, y1, h, t2,
-                              a_g, b_g, a_u, b_u, a_d, b_d)
+                              a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, brp, t_rb, seg1)
         ctx.base = base
-        ctx.meta = (k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd)
+        ctx.meta = (k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd, rr, rpr, scale_r)
         ctx.logits_supplied = logits_supplied
+        ctx.fuse_main_grad = fuse_main_grad
         ctx.mark_non_differentiable(idx, plan.counts, plan.status)
         return y, idx, plan.counts, plan.status
 
     @staticmethod
     def backward(ctx, dy, *unused: Any):
         (x, idx, w, dest, rows, row_prob, seg, t1, y1, h, t2,
-         a_g, b_g, a_u, b_u, a_d, b_d) = ctx.saved_tensors
+         a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, brp, t_rb, seg1) = ctx.saved_tensors
         base: FrozenExperts = ctx.base
-        k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd = ctx.meta
+        k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd, rr, rpr, scale_r = ctx.meta
         e, f = base.num_experts, base.ffn
         t = x.shape[0]
         m = t * k
@@ -150,7 +226,7 @@ class _MoELoRALayerFn(torch.autograd.Function):
         h_dim = base.hidden
         # backward operand layouts in one launch: B_d and A_d rank-padded, the
         # block-diagonal [[s_g B_g, 0], [0, s_u B_u]] (g1 = [s_g dg B_g^T | s_u du B_u^T]
-        # as one product, dy1 read once) and [A_g | A_u]
+        # as one product, dy1 read once), [A_g | A_u] and A_r
         bdp = b_d if rd == rpd and b_d.is_contiguous() else dy.new_empty((e, rpd, h_dim))
         adp = a_d if rd == rpd and a_d.is_contiguous() else dy.new_empty((e, f, rpd))
         gb = dy.new_empty((e, rpg + rpu, 2 * f))
@@ -162,6 +238,10 @@ class _MoELoRALayerFn(torch.autograd.Function):
             items.append((bdp, b_d, 1.0))
         if adp is not a_d:
             items.append((adp, a_d, 1.0))
+        ar_dx = None
+        if rr and not ctx.logits_supplied:
+            ar_dx = dy.new_empty((1, h_dim, rpr))  # A_r, rank zero-padded
+            items.append((ar_dx, a_r.unsqueeze(0), 1.0))
         ops.pack(*items)
         # FC2 data gradient with the SwiGLU backward in its epilogue
         g2 = ops.grouped_gemm(dy, bdp, seg, e, m=m, a_rows=rows, alpha=sd)
@@ -172,37 +252,59 @@ class _MoELoRALayerFn(torch.autograd.Function):
         # router: softmax backward over the k selected logits
         dl, dlogits = ops.router_backward(dp_part, dest, w, idx, e,
                                           dense=ctx.logits_supplied and ctx.needs_input_grad[1])
+        fuse = ctx.fuse_main_grad
+        router_grads = [None, None]
         if not ctx.logits_supplied:
-            dx = ops.combine(dx_perm, dest, t, dl=dl, idx=idx, w_r=base.w_r)
+            addend = None
+            if rr:   # router LoRA: dx += g_r A_r^T with g_r = s_r dlogits B_r^T
+                g_r, dlog = ops.router_lora_grad(dl, idx, brp[0], scale_r)
+                addend = ops.grouped_gemm(g_r, ar_dx, seg1, 1, m=t)
+                router_grads = (_land_wgrad(x, g_r, seg1, 1, [(a_r, 0)], fuse_main_grad=fuse)
+                                + _land_wgrad(dlog, t_rb, seg1, 1, [(b_r, 0)], alpha=scale_r,
+                                              transpose_out=True, fuse_main_grad=fuse))
+            dx = ops.combine(dx_perm, dest, t, dl=dl, idx=idx, w_r=base.w_r, addend=addend)
         else:
             dx = ops.combine(dx_perm, dest, t)
-        # LoRA weight gradients: fp32 accumulation, rounded once to the parameter dtype
-        od = torch.bfloat16 if a_g.dtype == torch.bfloat16 else torch.float32
-        da1 = ops.grouped_wgrad(x, g1, seg, e, l_rows=rows, out_dtype=od)             # [E,H,RP1]
-        dbg = ops.grouped_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, alpha=sg, transpose_out=True,
-                                out_dtype=od)
-        dbu = ops.grouped_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, alpha=su, transpose_out=True,
-                                out_dtype=od)
-        dad = ops.grouped_wgrad(h, g2, seg, e, out_dtype=od)                           # [E,F,RPd]
-        dbd = ops.grouped_wgrad(dy, t2, seg, e, alpha=sd, l_rows=rows, transpose_out=True,
-                                out_dtype=od)
-        return (dx, dlogits, None,
-                da1[:, :, :rg].to(a_g.dtype), dbg[:, :rg].to(b_g.dtype),
-                da1[:, :, rpg:rpg + ru].to(a_u.dtype), dbu[:, :ru].to(b_u.dtype),
-                dad[:, :, :rd].to(a_d.dtype), dbd[:, :rd].to(b_d.dtype),
-                None, None, None)
+        # LoRA weight gradients: fp32 accumulation, landed in fp32 main_grad or
+        # rounded once to the parameter dtype
+        gag, gau = _land_wgrad(x, g1, seg, e, [(a_g, 0), (a_u, rpg)], l_rows=rows,
+                               fuse_main_grad=fuse)
+        (gbg,) = _land_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, [(b_g, 0)], alpha=sg,
+                             transpose_out=True, fuse_main_grad=fuse)
+        (gbu,) = _land_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, [(b_u, 0)], alpha=su,
+                             transpose_out=True, fuse_main_grad=fuse)
+        (gad,) = _land_wgrad(h, g2, seg, e, [(a_d, 0)], fuse_main_grad=fuse)
+        (gbd,) = _land_wgrad(dy, t2, seg, e, [(b_d, 0)], alpha=sd, l_rows=rows,
+                             transpose_out=True, fuse_main_grad=fuse)
+        return (dx, dlogits, None, gag, gbg, gau, gbu, gad, gbd, router_grads[0], router_grads[1],
+                None, None, None, None, None)
 
 
 def moe_lora_layer(x, base: FrozenExperts, a_g, b_g, a_u, b_u, a_d, b_d, *, k: int,
                    scales: tuple[float, float, float], logits: torch.Tensor | None = None,
-                   target: torch.Tensor | None = None):
+                   target: torch.Tensor | None = None,
+                   router_lora: tuple[torch.Tensor, torch.Tensor, float] | None = None,
+                   fuse_main_grad: bool = False):
     """Functional layer.  Returns (y [T,H] bf16, idx [T,k], counts [E], status [1]).
 
     ``logits`` (fp32 [T,E]) replaces the router gating linear; ``target``
     (int [T,k]) replays routes.  ``status`` counts rejected replay ids.
+    ``router_lora = (A_r [H,r], B_r [r,E], scale)`` adds s (x A_r) B_r to the
+    router logits (fp32).  ``fuse_main_grad`` accumulates the LoRA gradients
+    into each factor's fp32 ``main_grad`` instead of returning them.
     """
     if x.dtype != torch.bfloat16 or x.device.type != "cuda":
         raise ValueError("x must be a bf16 CUDA tensor")
     if logits is None and base.w_r is None:
         raise ValueError("either router weights or logits are required")
-    return _MoELoRALayerFn.apply(x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, base, k, scales)
+    a_r = b_r = None
+    scale_r = 1.0
+    if router_lora is not None:
+        if logits is not None:
+            raise ValueError("router_lora needs the router gating linear (logits must be None)")
+        a_r, b_r, scale_r = router_lora
+        if a_r.dim() != 2 or b_r.dim() != 2 or a_r.shape[1] != b_r.shape[0] \
+                or a_r.shape[0] != base.hidden or b_r.shape[1] != base.num_experts:
+            raise ValueError("router LoRA must be A_r [H, r], B_r [r, E]")
+    return _MoELoRALayerFn.apply(x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, base,
+                                 k, scales, float(scale_r), bool(fuse_main_grad))

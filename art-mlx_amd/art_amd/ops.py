@@ -140,8 +140,10 @@ def permute(x: torch.Tensor, dest: torch.Tensor, num_rows: int) -> torch.Tensor:
 
 def combine(y_perm: torch.Tensor, dest: torch.Tensor, num_tokens: int, *,
             wgt: torch.Tensor | None = None, dl: torch.Tensor | None = None,
-            idx: torch.Tensor | None = None, w_r: torch.Tensor | None = None) -> torch.Tensor:
-    _cuda(y_perm, dest, wgt, dl, idx, w_r)
+            idx: torch.Tensor | None = None, w_r: torch.Tensor | None = None,
+            addend: torch.Tensor | None = None) -> torch.Tensor:
+    """y[t] = sum_j wgt[t,j] y_perm[dest[t,j]] (+ sum_j dl[t,j] w_r[idx[t,j]]) (+ addend[t])."""
+    _cuda(y_perm, dest, wgt, dl, idx, w_r, addend)
     _need(y_perm.dtype == torch.bfloat16 and y_perm.dim() == 2, "y_perm must be bf16 [M, H]")
     y_perm = y_perm.contiguous()
     h = y_perm.shape[1]
@@ -149,11 +151,15 @@ def combine(y_perm: torch.Tensor, dest: torch.Tensor, num_tokens: int, *,
     if w_r is not None:
         _need(w_r.dtype == torch.bfloat16 and w_r.shape[1] == h, "w_r must be bf16 [E, H]")
         w_r = w_r.contiguous()
+    if addend is not None:
+        _need(addend.dtype == torch.bfloat16 and addend.shape == (num_tokens, h),
+              "addend must be bf16 [T, H]")
+        addend = addend.contiguous()
     call("art_moe_combine", ptr(y_perm), ptr(dest.contiguous()),
          ptr(wgt.contiguous() if wgt is not None else None),
          ptr(dl.contiguous() if dl is not None else None),
          ptr(idx.contiguous() if idx is not None else None), ptr(w_r),
-         num_tokens, dest.shape[1], h, ptr(y), stream_ptr(y.device))
+         ptr(addend), num_tokens, dest.shape[1], h, ptr(y), stream_ptr(y.device))
     return y
 
 
@@ -243,13 +249,16 @@ def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_expe
                   alpha: float = 1.0, l_rows: torch.Tensor | None = None,
                   r_rows: torch.Tensor | None = None, transpose_out: bool = False,
                   out: torch.Tensor | None = None, accumulate: bool = False,
-                  out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                  out_dtype: torch.dtype = torch.float32, out2: torch.Tensor | None = None,
+                  q_split: int = 0) -> torch.Tensor:
     """out[e] = alpha * Lm_e^T @ R_e ([E,P,Q]; [E,Q,P] with transpose_out).
 
     fp32 accumulation; the output is fp32 or, with ``out_dtype=torch.bfloat16``,
     the fp32 sum rounded once to bf16.  ``accumulate`` adds to an fp32 ``out``.
+    With ``out2`` (same orientation and dtype as ``out``), columns q >= q_split
+    land in ``out2`` at q - q_split and ``out`` holds the first q_split.
     """
-    _cuda(lm, r, seg, l_rows, r_rows, out)
+    _cuda(lm, r, seg, l_rows, r_rows, out, out2)
     p, q = lm.shape[-1], r.shape[-1]
     if out is None:
         shape = (num_experts, q, p) if transpose_out else (num_experts, p, q)
@@ -260,13 +269,21 @@ def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_expe
         mode = _lib.WGRAD_ACCUMULATE
     else:
         mode = _lib.WGRAD_STORE_BF16 if out.dtype == torch.bfloat16 else _lib.WGRAD_STORE
-    if transpose_out:
-        o_es, o_ps, o_qs = out.stride(0), out.stride(2), out.stride(1)
-    else:
-        o_es, o_ps, o_qs = out.stride(0), out.stride(1), out.stride(2)
+    def strides(o):
+        if o is None:
+            return 0, 0, 0
+        return (o.stride(0), o.stride(2), o.stride(1)) if transpose_out else \
+            (o.stride(0), o.stride(1), o.stride(2))
+    o_es, o_ps, o_qs = strides(out)
+    o2_es, o2_ps, o2_qs = strides(out2)
+    if out2 is not None:
+        _need(0 < q_split < q and out2.dtype == out.dtype, "out2 needs 0 < q_split < Q, same dtype")
+        qdim = 1 if transpose_out else 2
+        _need(out.shape[qdim] >= q_split and out2.shape[qdim] >= q - q_split,
+              "split outputs too small")
     call("art_moe_grouped_wgrad", ptr(lm), _rowmajor(lm, "Lm"), ptr(l_rows), ptr(r), _rowmajor(r, "R"),
          ptr(r_rows), ptr(seg), num_experts, p, q, float(alpha), ptr(out), o_es, o_ps, o_qs,
-         mode, stream_ptr(lm.device))
+         ptr(out2), int(q_split), o2_es, o2_ps, o2_qs, mode, stream_ptr(lm.device))
     return out
 
 
@@ -289,7 +306,7 @@ def transposed(src: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
 
 
 def pack(*items) -> None:
-    """Batched strided copies in one launch (at most 8 per call).
+    """Batched strided copies in one launch (at most 16 per call).
 
     Each item is ``(dst, src, scale)``: ``dst`` an [E, R, C] bf16 view with a
     contiguous last dimension, ``src`` an [E, Rs, Cs] bf16 view with any
@@ -318,3 +335,32 @@ def pack(*items) -> None:
         dev = dst.device
     if items:
         call("art_moe_pack", ctypes.cast(descs, ctypes.c_void_p), len(items), stream_ptr(dev))
+
+
+# ------------------------------------------------------------- router LoRA
+def router_lora_apply(t_r: torch.Tensor, b_t: torch.Tensor, logits: torch.Tensor,
+                      scale: float, *, want_bf16: bool = False) -> torch.Tensor | None:
+    """logits += scale * t_r @ B_T in fp32 (in place); returns bf16(t_r) if asked."""
+    _cuda(t_r, b_t, logits)
+    t, r = t_r.shape
+    e = logits.shape[1]
+    _need(t_r.dtype == torch.float32 and t_r.is_contiguous(), "t_r must be contiguous fp32 [T, r]")
+    _need(b_t.dtype == torch.bfloat16 and b_t.shape == (r, e), "B_T must be bf16 [r, E]")
+    _need(logits.dtype == torch.float32 and logits.is_contiguous() and logits.shape[0] == t,
+          "logits must be contiguous fp32 [T, E]")
+    t_bf = torch.empty((t, r), dtype=torch.bfloat16, device=t_r.device) if want_bf16 else None
+    call("art_moe_router_lora_apply", ptr(t_r), t, r, ptr(b_t.contiguous()), e, float(scale),
+         ptr(logits), ptr(t_bf), stream_ptr(t_r.device))
+    return t_bf
+
+
+def router_lora_grad(dl: torch.Tensor, idx: torch.Tensor, b_t: torch.Tensor, scale: float):
+    """(g bf16 [T, r], dlogits bf16 [T, E]) of the router LoRA backward."""
+    _cuda(dl, idx, b_t)
+    t, k = dl.shape
+    r, e = b_t.shape
+    g = torch.empty((t, r), dtype=torch.bfloat16, device=dl.device)
+    dlog = torch.empty((t, e), dtype=torch.bfloat16, device=dl.device)
+    call("art_moe_router_lora_grad", ptr(dl.contiguous()), ptr(idx.contiguous()), t, k,
+         ptr(b_t.contiguous()), r, e, float(scale), ptr(g), ptr(dlog), stream_ptr(dl.device))
+    return g, dlog

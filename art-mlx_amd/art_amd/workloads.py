@@ -4,7 +4,8 @@ benchmark specification, numbered C0..C4).
 C0  tiny fp32-reference case: T=256, H=256, E=8, k=2, F=512, r=8, alpha=16
 C1  Qwen3-30B-A3B expert layer: T=8192, H=2048, E=128, k=8, F=768, r=16
 C2  C1 shapes with routing replay: Zipf(1.2) expert ids, Dirichlet(1) weights
-C3  long context: T=32768, r=64
+C3  long context: T=32768, r=64, router LoRA rank 64 (A_r [H,64], B_r [64,E]),
+    LoRA gradients accumulated in fp32
 C4  wide layer: H=4096, F=1536, T=16384, r=32 (fp8 base weights upstream;
     here bf16 base weights until the fp8 path lands)
 
@@ -45,6 +46,7 @@ class LayerConfig:
     alpha: float = 32.0
     replay: bool = False
     note: str = ""
+    router_r: int = 0       # router LoRA rank (0: none)
 
     @property
     def scale(self) -> float:
@@ -62,8 +64,11 @@ class LayerConfig:
         base = 2 * (base_fc1 + base_fc2)                       # fwd + dgrad
         lora = 3 * (2 * m * r * (h + f) * 2 + 2 * m * r * (f + h))  # gate, up, down; fwd + 2x bwd
         router = 4 * t * h * e                                 # fwd + dx
-        return {"base": base, "lora": lora, "router": router, "fc1_fwd": base_fc1,
-                "fc2_fwd": base_fc2, "total": base + lora + router}
+        rr = self.router_r
+        router_lora = 6 * t * rr * (h + e)                     # fwd + dx + dA_r/dB_r
+        return {"base": base, "lora": lora, "router": router, "router_lora": router_lora,
+                "fc1_fwd": base_fc1, "fc2_fwd": base_fc2,
+                "total": base + lora + router + router_lora}
 
     def dispatch_combine_bytes(self, b: int = 2) -> int:
         """HBM bytes of dispatch + combine, fwd + bwd, with materialised permutes."""
@@ -77,8 +82,8 @@ CONFIGS = {
                       note="Qwen3-30B-A3B expert layer"),
     "C2": LayerConfig("C2", T=8192, H=2048, E=128, k=8, F=768, r=16, replay=True,
                       note="C1 + Zipf(1.2) routing replay"),
-    "C3": LayerConfig("C3", T=32768, H=2048, E=128, k=8, F=768, r=64,
-                      note="long-context GRPO step"),
+    "C3": LayerConfig("C3", T=32768, H=2048, E=128, k=8, F=768, r=64, router_r=64,
+                      note="long-context GRPO step, router LoRA, fp32 LoRA grad accumulation"),
     "C4": LayerConfig("C4", T=16384, H=4096, E=128, k=8, F=1536, r=32,
                       note="wide layer"),
 }
@@ -149,6 +154,9 @@ def make_inputs(cfg: LayerConfig, device="cpu", seed: int = 0, dtype=torch.bfloa
         "a_u": rnd(e, h, r, std=0.01), "b_u": rnd(e, r, f, std=0.01),
         "a_d": rnd(e, f, r, std=0.01), "b_d": rnd(e, r, h, std=0.01),
     }
+    if cfg.router_r:
+        lora["a_r"] = rnd(h, cfg.router_r, std=0.01)
+        lora["b_r"] = rnd(cfg.router_r, e, std=0.01)
     dy = rnd(t, h)
     logits = target = None
     if cfg.replay:

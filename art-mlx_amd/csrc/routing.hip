@@ -291,7 +291,7 @@ constexpr int kMaxK = 32;
 __global__ __launch_bounds__(256) void combine_kernel(
     const U4 *__restrict__ yp, const int32_t *__restrict__ dest, const float *__restrict__ wgt,
     const float *__restrict__ dl, const int32_t *__restrict__ idx, const U4 *__restrict__ w_r,
-    int64_t T, int k, int H8, U4 *__restrict__ y) {
+    const U4 *__restrict__ addend, int64_t T, int k, int H8, U4 *__restrict__ y) {
   const int lane = lane_id();
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -328,7 +328,85 @@ __global__ __launch_bounds__(256) void combine_kernel(
         for (int i = 0; i < 8; ++i) acc[i] += lj * f[i];
       }
     }
+    if (addend && on) {
+      float f[8];
+      unpack8(addend[t * H8 + c], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += f[i];
+    }
     if (on) y[t * H8 + c] = pack8(acc);
+  }
+}
+
+// ---------------------------------------------------------- router LoRA
+// One wavefront per 4 tokens, lanes over the E logit columns; t_r rows are
+// wave-uniform reads, B rows coalesced and L1/L2-resident (r*E*2 bytes).
+__global__ __launch_bounds__(256) void router_lora_apply_kernel(
+    const float *__restrict__ t_r, int64_t T, int r, const bf16 *__restrict__ b, int E,
+    float scale, float *__restrict__ logits, bf16 *__restrict__ t_bf16) {
+  const int lane = lane_id();
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+  if (t0 >= T) return;
+  const int nt = (int)(T - t0 < 4 ? T - t0 : 4);
+  const float *tr = t_r + t0 * r;
+  for (int e = lane; e < E; e += kWave) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < r; ++i) {
+      const float bv = (float)b[(int64_t)i * E + e];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (u < nt) acc[u] += tr[u * r + i] * bv;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (u < nt) logits[(t0 + u) * E + e] += scale * acc[u];
+  }
+  if (t_bf16)
+    for (int p = lane; p < nt * r; p += kWave) t_bf16[t0 * r + p] = (bf16)tr[p];
+}
+
+// B^T staged in LDS ([E][r] bf16) once per block; each wavefront then walks
+// its tokens: lane i of g sums the k selected columns of B, and the dense
+// bf16 dlogits row is written with lanes over E.
+constexpr int kLoraGradTokens = 64;  // tokens per workgroup
+
+__global__ __launch_bounds__(256) void router_lora_grad_kernel(
+    const float *__restrict__ dl, const int32_t *__restrict__ idx, int64_t T, int k,
+    const bf16 *__restrict__ b, int r, int E, float scale, bf16 *__restrict__ g,
+    bf16 *__restrict__ dlog) {
+  extern __shared__ bf16 bt[];
+  for (int p = threadIdx.x; p < r * E; p += blockDim.x) {
+    const int i = p / E, e = p - i * E;
+    bt[e * r + i] = b[p];
+  }
+  __syncthreads();
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int64_t tb = (int64_t)blockIdx.x * kLoraGradTokens;
+  const int64_t te = tb + kLoraGradTokens < T ? tb + kLoraGradTokens : T;
+  for (int64_t t = tb + wave; t < te; t += 4) {
+    const bool act = lane < k;
+    const int my_e = act ? idx[t * k + lane] : -1;
+    const float my_dl = act ? dl[t * k + lane] : 0.0f;
+    for (int i0 = 0; i0 < r; i0 += kWave) {
+      const int i = i0 + lane;
+      float acc = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const int e = __shfl(my_e, j, kWave);
+        const float lj = __shfl(my_dl, j, kWave);
+        if (e >= 0 && i < r) acc += lj * (float)bt[e * r + i];
+      }
+      if (i < r) g[t * r + i] = (bf16)(scale * acc);
+    }
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int e = e0 + lane;
+      float v = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const int ej = __shfl(my_e, j, kWave);
+        const float lj = __shfl(my_dl, j, kWave);
+        if (ej == e) v += lj;
+      }
+      if (e < E) dlog[t * E + e] = (bf16)v;
+    }
   }
 }
 
@@ -611,16 +689,47 @@ extern "C" int art_moe_permute(const void *x, const int32_t *dest, int64_t T, in
 }
 
 extern "C" int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
-                               const float *dl, const int32_t *idx, const void *w_r, int64_t T,
-                               int32_t k, int32_t H, void *y, void *stream) {
+                               const float *dl, const int32_t *idx, const void *w_r,
+                               const void *addend, int64_t T, int32_t k, int32_t H, void *y,
+                               void *stream) {
   clear_error();
   ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0,
               "combine: need H %% 8 == 0 and 1 <= k <= 32 (H=%d k=%d)", H, k);
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(y_perm && dest && y && (!w_r || (dl && idx)), "combine: null pointer");
   combine_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
-      (const U4 *)y_perm, dest, wgt, dl, idx, (const U4 *)w_r, T, k, H / 8, (U4 *)y);
+      (const U4 *)y_perm, dest, wgt, dl, idx, (const U4 *)w_r, (const U4 *)addend, T, k, H / 8,
+      (U4 *)y);
   return check_launch("combine");
+}
+
+extern "C" int art_moe_router_lora_apply(const float *t_r, int64_t T, int32_t r, const void *b,
+                                         int32_t E, float scale, float *logits, void *t_bf16,
+                                         void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && r >= 1 && E >= 1, "router_lora_apply: need T >= 0, r >= 1, E >= 1");
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(t_r && b && logits, "router_lora_apply: null pointer");
+  const int64_t waves = (T + 3) / 4;
+  router_lora_apply_kernel<<<dim3((unsigned)((waves + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      t_r, T, r, (const bf16 *)b, E, scale, logits, (bf16 *)t_bf16);
+  return check_launch("router_lora_apply");
+}
+
+extern "C" int art_moe_router_lora_grad(const float *dl, const int32_t *idx, int64_t T, int32_t k,
+                                        const void *b, int32_t r, int32_t E, float scale, void *g,
+                                        void *dlog, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && r >= 1 && E >= 1,
+              "router_lora_grad: need 1 <= k <= 32, r >= 1, E >= 1 (k=%d r=%d E=%d)", k, r, E);
+  ART_REQUIRE((int64_t)r * E <= 32768, "router_lora_grad: r * E must be <= 32768 (r=%d E=%d)", r, E);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(dl && idx && b && g && dlog, "router_lora_grad: null pointer");
+  const size_t lds = (size_t)r * E * sizeof(bf16);
+  router_lora_grad_kernel<<<dim3((unsigned)((T + kLoraGradTokens - 1) / kLoraGradTokens)), 256, lds,
+                            as_stream(stream)>>>(dl, idx, T, k, (const bf16 *)b, r, E, scale,
+                                                 (bf16 *)g, (bf16 *)dlog);
+  return check_launch("router_lora_grad");
 }
 
 extern "C" int art_moe_transpose(const void *src, int32_t E, int32_t R, int32_t C, int64_t s_es,

@@ -32,6 +32,9 @@ struct WArgs {
   float alpha;
   void *out;
   int64_t o_es, o_sp, o_sq;
+  void *out2;  // columns q >= q_split land here (column q - q_split)
+  int q_split;
+  int64_t o2_es, o2_sp, o2_sq;
   int mode;  // ART_MOE_WGRAD_STORE / _ACCUMULATE / _STORE_BF16
 };
 
@@ -117,12 +120,16 @@ __global__ __launch_bounds__(256) void wgrad_tn_kernel(const WArgs a) {
         const int pp = p0 + wave * (BP / 4) + i * 16 + g4 * 4 + v;
         const int qq = q0 + j * 16 + l16;
         if (pp < a.P && qq < a.Q) {
-          const int64_t off = (int64_t)e * a.o_es + (int64_t)pp * a.o_sp + (int64_t)qq * a.o_sq;
+          const bool second = a.out2 != nullptr && qq >= a.q_split;
+          void *base = second ? a.out2 : a.out;
+          const int64_t off = second
+              ? (int64_t)e * a.o2_es + (int64_t)pp * a.o2_sp + (int64_t)(qq - a.q_split) * a.o2_sq
+              : (int64_t)e * a.o_es + (int64_t)pp * a.o_sp + (int64_t)qq * a.o_sq;
           const float val = a.alpha * acc[i][j][v];
           if (a.mode == ART_MOE_WGRAD_STORE_BF16) {
-            ((bf16 *)a.out)[off] = (bf16)val;
+            ((bf16 *)base)[off] = (bf16)val;
           } else {
-            float *o = (float *)a.out + off;
+            float *o = (float *)base + off;
             *o = a.mode == ART_MOE_WGRAD_ACCUMULATE ? *o + val : val;
           }
         }
@@ -144,7 +151,8 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
                                      const void *r, int64_t ldr, const int32_t *r_rows,
                                      const int32_t *seg, int32_t E, int32_t P, int32_t Q,
                                      float alpha, void *out, int64_t o_es, int64_t o_ps,
-                                     int64_t o_qs, int32_t mode, void *stream) {
+                                     int64_t o_qs, void *out2, int32_t q_split, int64_t o2_es,
+                                     int64_t o2_ps, int64_t o2_qs, int32_t mode, void *stream) {
   clear_error();
   ART_REQUIRE(E >= 1 && E <= 65535, "grouped_wgrad: need 1 <= E <= 65535 (E=%d)", E);
   ART_REQUIRE(P > 0 && Q > 0 && P % 8 == 0 && Q % 8 == 0,
@@ -160,7 +168,11 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   a.l = (const bf16 *)lm; a.ldl = ldl; a.l_rows = l_rows;
   a.r = (const bf16 *)r; a.ldr = ldr; a.r_rows = r_rows;
   a.seg = seg; a.E = E; a.P = P; a.Q = Q; a.alpha = alpha;
+  ART_REQUIRE(!out2 || (q_split > 0 && q_split < Q),
+              "grouped_wgrad: split output needs 0 < q_split < Q (q_split=%d Q=%d)", q_split, Q);
   a.out = out; a.o_es = o_es; a.o_sp = o_ps; a.o_sq = o_qs; a.mode = mode;
+  a.out2 = out2; a.q_split = out2 ? q_split : Q;
+  a.o2_es = o2_es; a.o2_sp = o2_ps; a.o2_sq = o2_qs;
   hipStream_t s = as_stream(stream);
   if (Q <= 16) return launch_wgrad<128, 16>(a, s);
   if (Q <= 32) return launch_wgrad<128, 32>(a, s);

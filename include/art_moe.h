@@ -127,11 +127,15 @@ int art_moe_permute(const void *x, const int32_t *dest, int64_t T, int32_t k,
 
 /* y[t, :] = sum_j (wgt ? wgt[t,j] : 1) * y_perm[dest[t,j], :]
  *           + (w_r ? sum_j dl[t,j] * w_r[idx[t,j], :] : 0)
- * fp32 accumulation in slot order j = 0..k-1, bf16 out.  With w_r == NULL
- * this is moe_utils.unpermute (combine); with w_r it also adds the router
- * input gradient dl @ W_r restricted to the k selected experts. */
+ *           + (addend ? addend[t, :] : 0)
+ * fp32 accumulation in slot order j = 0..k-1, then the router term, then the
+ * addend; bf16 out (one rounding).  With w_r == NULL this is
+ * moe_utils.unpermute (combine); with w_r it also adds the router input
+ * gradient dl @ W_r restricted to the k selected experts; the bf16 [T, H]
+ * addend carries further input-gradient terms (the router LoRA's). */
 int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
                     const float *dl, const int32_t *idx, const void *w_r,
+                    const void *addend,
                     int64_t T, int32_t k, int32_t H, void *y, void *stream);
 
 /* ------------------------------------------------------------- grouped GEMM */
@@ -205,14 +209,44 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
  * fp32 out, _STORE_BF16 writes bf16 out (one rounding of the fp32 sum: the
  * parameter-dtype gradient the reference returns).
  * Experts with no rows get zeros (or keep out when accumulating).
+ * Split output: with out2 != NULL, columns q < q_split land in out and
+ * columns q >= q_split in out2 at column q - q_split (strides o2_*), e.g. the
+ * gate and up halves of a fused [A_g | A_u] gradient into two buffers.
  * Replaces: QuACK varlen-K GEMMs for grad_A / grad_B
  * (cute_grouped_lora_quack.py:301-334, 411-431, 585-616). */
 int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
                           const void *r, int64_t ldr, const int32_t *r_rows,
                           const int32_t *seg, int32_t E, int32_t P, int32_t Q,
                           float alpha, void *out, int64_t o_es,
-                          int64_t o_ps, int64_t o_qs, int32_t mode,
-                          void *stream);
+                          int64_t o_ps, int64_t o_qs, void *out2,
+                          int32_t q_split, int64_t o2_es, int64_t o2_ps,
+                          int64_t o2_qs, int32_t mode, void *stream);
+
+/* ------------------------------------------------------------ router LoRA
+ * No counterpart in the reference, which puts no LoRA on the router
+ * (src/art/megatron/lora.py:1678-1889 wraps attention, GDN and experts only).
+ * Closed form of this build: logits = x W_r^T + s (x A_r) B_r, A_r = A_T
+ * [H, r], B_r = B_T [r, E], kept in fp32 like the router linear
+ * (src/art/megatron/provider.py:605). */
+
+/* logits[t*E + e] += scale * sum_i t_r[t*r + i] * b[i*E + e]   (fp32)
+ * t_r fp32 [T, r] = x A_r from an fp32-output product; b bf16 [r, E].
+ * t_bf16 (optional) [T, r] receives t_r rounded to bf16 (operand of the
+ * B_r gradient). */
+int art_moe_router_lora_apply(const float *t_r, int64_t T, int32_t r,
+                              const void *b, int32_t E, float scale,
+                              float *logits, void *t_bf16, void *stream);
+
+/* Backward pieces from the compact router gradient dl [T,k] (fp32) over the
+ * selected experts idx [T,k] (slots with idx < 0 are skipped):
+ *   g[t*r + i]    = bf16(scale * sum_j dl[t,j] * b[i*E + idx[t,j]])
+ *                   (dx += g A_r^T, dA_r = x^T g)
+ *   dlog[t*E + e] = bf16(sum_{j: idx[t,j] = e} dl[t,j])
+ *                   (dense dlogits, dB_r = scale * t_r^T dlog)
+ * r * E <= 32768. */
+int art_moe_router_lora_grad(const float *dl, const int32_t *idx, int64_t T,
+                             int32_t k, const void *b, int32_t r, int32_t E,
+                             float scale, void *g, void *dlog, void *stream);
 
 /* Batched strided transpose with scale:
  *   dst[e*d_es + c*d_ld + r] = bf16(scale * src[e*s_es + r*s_ld + c])
@@ -236,7 +270,7 @@ typedef struct {
   float scale;
 } art_moe_pack_desc;
 
-#define ART_MOE_PACK_MAX 8
+#define ART_MOE_PACK_MAX 16
 
 /* Up to ART_MOE_PACK_MAX strided copies in one launch: builds the padded,
  * transposed and scaled LoRA operand layouts of the grouped products (zero

@@ -7,7 +7,9 @@ autograd of this forward.
 Reference functions restated (file:line under /root/reference):
 * ``router_logits``     megatron ``router_gating_linear`` with fp32 router:
                         src/art/megatron/runtime/bridge_runtime.py:775-798,
-                        src/art/megatron/provider.py:605.
+                        src/art/megatron/provider.py:605; optional router
+                        LoRA term s (x A_r) B_r (closed form only: no
+                        counterpart in the reference).
 * ``routing``           TopKRouter.routing contract,
                         tests/unit/test_moe_routing_replay.py:181-205;
                         src/art/megatron/dsv4/layer.py:139-191 (gather/scatter).
@@ -36,6 +38,8 @@ Pinning (tests/test_oracle_layer.py):
   output equals one dense SwiGLU MLP applied to every token, because the k
   renormalised weights of a token sum to one.
 * weighted_swiglu: finite differences and the closed form at g = 0.
+* router LoRA: equals the plain router with the merged weight
+  W_r + s (A_r B_r)^T, and finite differences through the layer.
 """
 from __future__ import annotations
 
@@ -47,9 +51,19 @@ import torch
 from . import routing as _routing
 
 
-def router_logits(x: torch.Tensor, w_r: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
-    """logits = x.to(fp32) @ W_r.to(fp32).T  ([T,H] x [E,H] -> [T,E])."""
-    return x.to(dtype) @ w_r.to(dtype).t()
+def router_logits(x: torch.Tensor, w_r: torch.Tensor, dtype=torch.float32, *,
+                  a_r: torch.Tensor | None = None, b_r: torch.Tensor | None = None,
+                  scale_r: float = 1.0) -> torch.Tensor:
+    """logits = x.to(fp32) @ W_r.to(fp32).T  ([T,H] x [E,H] -> [T,E]),
+    plus the router LoRA term ``scale_r * (x @ A_r) @ B_r`` (A_r = A_T [H,r],
+    B_r = B_T [r,E]) when given.  The reference has no router LoRA (its LoRA
+    wraps attention, GDN and experts only, src/art/megatron/lora.py:1678-1889);
+    this closed form is the definition used here."""
+    xd = x.to(dtype)
+    out = xd @ w_r.to(dtype).t()
+    if a_r is not None:
+        out = out + scale_r * ((xd @ a_r.to(dtype)) @ b_r.to(dtype))
+    return out
 
 
 def routing(logits: torch.Tensor, k: int, target: torch.Tensor | None = None):
@@ -151,6 +165,9 @@ class LayerParams:
     scale_g: float
     scale_u: float
     scale_d: float
+    a_r: torch.Tensor | None = None     # router LoRA A_T [H, r_r]
+    b_r: torch.Tensor | None = None     # router LoRA B_T [r_r, E]
+    scale_r: float = 1.0
 
 
 def moe_lora_layer(x: torch.Tensor, p: LayerParams, k: int, *,
@@ -163,7 +180,7 @@ def moe_lora_layer(x: torch.Tensor, p: LayerParams, k: int, *,
     """
     xw = x.to(dtype)
     if logits is None:
-        logits = router_logits(xw, p.w_r, dtype)
+        logits = router_logits(xw, p.w_r, dtype, a_r=p.a_r, b_r=p.b_r, scale_r=p.scale_r)
     else:
         logits = logits.to(dtype)
     num_experts = p.w1.shape[0]

@@ -239,7 +239,7 @@ def test_pack_layouts(device):
     assert torch.equal(p2.cpu(), r16(e2))
     assert torch.equal(blk.cpu(), r16(e3))
     with pytest.raises(ValueError):
-        ops.pack(*[(p2, None, 0.0)] * 9)
+        ops.pack(*[(p2, None, 0.0)] * 17)
 
 
 @pytest.mark.parametrize("e,h,f,r", [(4, 256, 192, 16), (3, 512, 96, 12), (2, 136, 64, 64)])

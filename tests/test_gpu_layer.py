@@ -146,3 +146,74 @@ def test_layer_c1_full_size_token_subset(device):
     got_sub["y"] = got["y"][subset]
     got_sub["dx"] = got["dx"][subset]
     _compare(got_sub, ref, ["y", "dx"] + ["d" + n for n in NAMES])
+
+
+def _gpu_layer_router_lora(inp, device, *, fuse=False, main_grads=None, tokens_dy=None):
+    from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
+    cfg = inp.cfg
+    base = FrozenExperts.build(inp.w_r.to(device), inp.w1.to(device), inp.w2.to(device))
+    names = NAMES + ("a_r", "b_r")
+    lora = {n: inp.lora[n].to(device).requires_grad_() for n in names}
+    if main_grads is not None:
+        for n in names:
+            lora[n].main_grad = main_grads[n]
+    x = inp.x.to(device).requires_grad_()
+    s = cfg.scale
+    y, idx, counts, status = moe_lora_layer(
+        x, base, *(lora[n] for n in NAMES), k=cfg.k, scales=(s, s, s),
+        router_lora=(lora["a_r"], lora["b_r"], cfg.alpha / cfg.router_r), fuse_main_grad=fuse)
+    y.backward(inp.dy.to(device) if tokens_dy is None else tokens_dy.to(device))
+    torch.cuda.synchronize()
+    out = {"y": y.detach().cpu(), "idx": idx.cpu(), "counts": counts.cpu(), "dx": x.grad.cpu()}
+    for n in names:
+        out["d" + n] = None if lora[n].grad is None else lora[n].grad.cpu()
+        out["added_" + n] = getattr(lora[n], "grad_added_to_main_grad", False)
+    return out
+
+
+def test_layer_c3_router_lora(device):
+    """C3 widths (r=64, router LoRA rank 64) on 512 tokens: router logits with
+    the LoRA term within 1e-5; y, dx and all eight LoRA gradients within 2e-2."""
+    from art_amd.megatron.moe_layer import router_logits
+    print("layer C3 router LoRA T=512", flush=True)
+    inp = _small("C3", 512)
+    cfg = inp.cfg
+    sr = cfg.alpha / cfg.router_r
+    lg = router_logits(inp.x.to(device), inp.w_r.to(device),
+                       router_lora=(inp.lora["a_r"].to(device), inp.lora["b_r"].to(device), sr)).cpu()
+    lg_ref = OL.router_logits(inp.x, inp.w_r, a_r=inp.lora["a_r"], b_r=inp.lora["b_r"], scale_r=sr)
+    assert rel(lg, lg_ref) < 1e-5
+    got = _gpu_layer_router_lora(inp, device)
+    assert np.array_equal(got["idx"].numpy(), R.topk_indices(lg.numpy(), cfg.k))
+    x = inp.x.float().requires_grad_()
+    names = NAMES + ("a_r", "b_r")
+    leaves = {n: inp.lora[n].float().requires_grad_() for n in names}
+    p = OL.LayerParams(w_r=inp.w_r, w1=inp.w1, w2=inp.w2, scale_g=cfg.scale, scale_u=cfg.scale,
+                       scale_d=cfg.scale, scale_r=sr, **leaves)
+    y, _ = OL.moe_lora_layer(x, p, cfg.k, target=got["idx"].long())
+    y.backward(inp.dy.float())
+    ref = {"y": y.detach(), "dx": x.grad, **{"d" + n: leaves[n].grad for n in names}}
+    _compare(got, ref, ["y", "dx"] + ["d" + n for n in names])
+
+
+@pytest.mark.parametrize("cfg_name", ["C3", "C0"])
+def test_layer_fused_main_grad_accumulation(device, cfg_name):
+    """Gradients accumulated into fp32 main_grad: one call rounds to exactly the
+    returned bf16 gradients; a second call doubles them exactly (fixed-order
+    fp32 sums).  C0's rank 8 exercises the padded-rank landing path."""
+    import dataclasses
+    from art_amd.workloads import CONFIGS, make_inputs
+    print(f"fused main_grad {cfg_name}", flush=True)
+    cfg = dataclasses.replace(CONFIGS[cfg_name], router_r=16)
+    inp = make_inputs(cfg, "cpu", seed=1, T=256)
+    names = NAMES + ("a_r", "b_r")
+    plain = _gpu_layer_router_lora(inp, device)
+    mg = {n: torch.zeros(inp.lora[n].shape, dtype=torch.float32, device=device) for n in names}
+    first = _gpu_layer_router_lora(inp, device, fuse=True, main_grads=mg)
+    snap = {n: mg[n].clone() for n in names}
+    _gpu_layer_router_lora(inp, device, fuse=True, main_grads=mg)
+    assert torch.equal(first["dx"], plain["dx"])
+    for n in names:
+        assert first["d" + n] is None and first["added_" + n], n
+        assert torch.equal(snap[n].to(torch.bfloat16).cpu(), plain["d" + n]), n
+        assert torch.equal(mg[n], 2 * snap[n]), n

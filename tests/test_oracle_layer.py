@@ -141,3 +141,33 @@ def test_layer_zero_tokens():
     y, aux = L.moe_lora_layer(torch.zeros(0, 8, dtype=D), p, 2, dtype=D)
     assert y.shape == (0, 8)
     assert aux["plan"]["counts"].tolist() == [0, 0, 0]
+
+
+def test_router_lora_equals_merged_router_weight():
+    """x W^T + s (x A) B == x (W + s (A B)^T)^T: pins operand order and scale."""
+    t, h, e, rr = 7, 6, 5, 3
+    x = _rand(t, h, seed=20)
+    w = _rand(e, h, seed=21)
+    a = _rand(h, rr, seed=22)
+    b = _rand(rr, e, seed=23)
+    got = L.router_logits(x, w, D, a_r=a, b_r=b, scale_r=0.75)
+    merged = L.router_logits(x, w + 0.75 * (a @ b).t(), D)
+    assert torch.allclose(got, merged, atol=1e-12)
+    assert torch.allclose(L.router_logits(x, w, D, a_r=a, b_r=torch.zeros_like(b), scale_r=2.0),
+                          L.router_logits(x, w, D), atol=0)
+
+
+def test_layer_gradcheck_router_lora():
+    e, h, f, r, t, k = 4, 4, 3, 2, 5, 2
+    p = _params(e, h, f, r, seed=30)
+    p.a_r = _rand(h, 3, seed=31).requires_grad_()
+    p.b_r = _rand(3, e, seed=32).requires_grad_()
+    p.scale_r = 0.5
+    x = _rand(t, h, seed=33).requires_grad_()
+
+    def fn(x, a_r, b_r):
+        p.a_r, p.b_r = a_r, b_r
+        y, _ = L.moe_lora_layer(x, p, k, dtype=D)
+        return y
+
+    assert torch.autograd.gradcheck(fn, (x, p.a_r, p.b_r), eps=1e-6, atol=1e-6)
