@@ -21,7 +21,7 @@ ART_MOE_OK = 0
 ART_MOE_ERR_INVALID_ARG = -1
 ART_MOE_ERR_UNSUPPORTED = -2
 ART_MOE_ERR_HIP = -3
-SEG_NBM = 4
+SEG_NBM = 5
 PACK_MAX = 16
 WGRAD_STORE = 0
 WGRAD_ACCUMULATE = 1
@@ -57,8 +57,10 @@ SIGNATURES = {
     "art_moe_dgrad_swiglu_parts": (_I32, [_I32]),
     "art_moe_fc2_dgrad_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I64, _P, _I32, _P, _I32, _I64,
                                         _I32, _I32, _P, _P, _P, _P, _P]),
-    "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I32, _I32, _F, _P,
-                                     _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P]),
+    "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32, _F,
+                                     _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P,
+                                     _SZ, _P]),
+    "art_moe_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
     "art_moe_pack": (_I32, [_P, _I32, _P]),
     "art_moe_router_lora_apply": (_I32, [_P, _I64, _I32, _P, _I32, _F, _P, _P, _P]),

@@ -250,13 +250,14 @@ def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_expe
                   r_rows: torch.Tensor | None = None, transpose_out: bool = False,
                   out: torch.Tensor | None = None, accumulate: bool = False,
                   out_dtype: torch.dtype = torch.float32, out2: torch.Tensor | None = None,
-                  q_split: int = 0) -> torch.Tensor:
+                  q_split: int = 0, m: int | None = None) -> torch.Tensor:
     """out[e] = alpha * Lm_e^T @ R_e ([E,P,Q]; [E,Q,P] with transpose_out).
 
     fp32 accumulation; the output is fp32 or, with ``out_dtype=torch.bfloat16``,
     the fp32 sum rounded once to bf16.  ``accumulate`` adds to an fp32 ``out``.
     With ``out2`` (same orientation and dtype as ``out``), columns q >= q_split
     land in ``out2`` at q - q_split and ``out`` holds the first q_split.
+    ``m`` (segment rows) defaults to the length of ``l_rows``, else of ``lm``.
     """
     _cuda(lm, r, seg, l_rows, r_rows, out, out2)
     p, q = lm.shape[-1], r.shape[-1]
@@ -281,9 +282,14 @@ def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_expe
         qdim = 1 if transpose_out else 2
         _need(out.shape[qdim] >= q_split and out2.shape[qdim] >= q - q_split,
               "split outputs too small")
+    if m is None:
+        m = l_rows.numel() if l_rows is not None else lm.shape[0]
+    ws_bytes = int(_lib.load().art_moe_wgrad_workspace_bytes(m, num_experts, p, q))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=lm.device) if ws_bytes else None
     call("art_moe_grouped_wgrad", ptr(lm), _rowmajor(lm, "Lm"), ptr(l_rows), ptr(r), _rowmajor(r, "R"),
-         ptr(r_rows), ptr(seg), num_experts, p, q, float(alpha), ptr(out), o_es, o_ps, o_qs,
-         ptr(out2), int(q_split), o2_es, o2_ps, o2_qs, mode, stream_ptr(lm.device))
+         ptr(r_rows), ptr(seg), num_experts, m, p, q, float(alpha), ptr(out), o_es, o_ps, o_qs,
+         ptr(out2), int(q_split), o2_es, o2_ps, o2_qs, mode, ptr(ws), ws_bytes,
+         stream_ptr(lm.device))
     return out
 
 

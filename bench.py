@@ -36,7 +36,8 @@ NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
 # ops whose time counts as GEMM (MFMA roofline) vs bandwidth-bound (HBM roofline)
 GEMM_OPS = ("grouped_gemm", "fc1_swiglu", "fc2_dgrad_swiglu", "grouped_wgrad")
 HBM_OPS = ("router_topk", "router_replay", "dispatch_plan", "combine", "router_backward",
-           "permute", "transpose_into", "segments_from_counts", "pack")
+           "permute", "transpose_into", "segments_from_counts", "pack", "router_lora_apply",
+           "router_lora_grad")
 
 
 class OpTimer:
@@ -89,7 +90,13 @@ def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0):
     dev = torch.device("cuda:0")
     inp = make_inputs(cfg, dev, seed=seed)
     base = moe_layer.FrozenExperts.build(inp.w_r, inp.w1, inp.w2)
-    lora = {n: inp.lora[n].requires_grad_() for n in NAMES}
+    names = NAMES + (("a_r", "b_r") if cfg.router_r else ())
+    lora = {n: inp.lora[n].requires_grad_() for n in names}
+    fuse = bool(cfg.router_r)   # C3: LoRA gradients accumulate in fp32 main_grad
+    if fuse:
+        for v in lora.values():
+            v.main_grad = torch.zeros(v.shape, dtype=torch.float32, device=dev)
+    router_lora = (lora["a_r"], lora["b_r"], cfg.alpha / cfg.router_r) if cfg.router_r else None
     x = inp.x.requires_grad_()
     s = cfg.scale
     logits = inp.logits if cfg.replay else None
@@ -103,7 +110,7 @@ def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0):
             v.grad = None
         y, _idx, _counts, _status = moe_layer.moe_lora_layer(
             x, base, *(lora[n] for n in NAMES), k=cfg.k, scales=(s, s, s), logits=logits,
-            target=target)
+            target=target, router_lora=router_lora, fuse_main_grad=fuse)
         y.backward(dy)
 
     for _ in range(warmup):
@@ -130,10 +137,12 @@ def cpu_baseline(cfg, tokens: int, iters: int, seed: int = 0):
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     inp = make_inputs(cfg, "cpu", seed=seed, T=tokens, dtype=torch.float32)
-    leaves = {n: inp.lora[n].requires_grad_() for n in NAMES}
+    names = NAMES + (("a_r", "b_r") if cfg.router_r else ())
+    leaves = {n: inp.lora[n].requires_grad_() for n in names}
     s = cfg.scale
     p = OL.LayerParams(w_r=None if cfg.replay else inp.w_r, w1=inp.w1, w2=inp.w2,
-                       scale_g=s, scale_u=s, scale_d=s, **leaves)
+                       scale_g=s, scale_u=s, scale_d=s,
+                       scale_r=cfg.alpha / cfg.router_r if cfg.router_r else 1.0, **leaves)
 
     def step():
         x = inp.x.clone().requires_grad_()
@@ -212,10 +221,12 @@ def main():
     fc1_tflops = fc1_flops / (fc1_ms * 1e-3) / 1e12
     gemm_ms = sum(tot[n] for n in GEMM_OPS) / args.steps
     hbm_ms = sum(tot[n] for n in HBM_OPS) / args.steps
-    gemm_flops = flops["base"] + flops["lora"] + flops["router"]
+    gemm_flops = flops["base"] + flops["lora"] + flops["router"] + flops["router_lora"]
     comb_ms = tot["combine"] / args.steps
     # combine fwd reads M rows, writes T rows; the dx un-permute also reads k router rows (L2)
     comb_bytes = 2 * (cfg.M * h * 2 + cfg.T * h * 2) + 2 * cfg.M * 4
+    disp_ops = ("router_topk", "router_replay", "dispatch_plan", "combine", "router_backward")
+    disp_ms = sum(tot[n] for n in disp_ops) / args.steps
     kernels = {name: round(tot[name] / args.steps, 4) for name in sorted(tot)}
 
     result = {
@@ -234,6 +245,8 @@ def main():
         "config": {"workload": f"{cfg.name}: {cfg.note}, layer fwd+bwd", "T": cfg.T, "H": h,
                    "E": cfg.E, "k": cfg.k, "F": f, "r": r, "alpha": cfg.alpha,
                    "routing": "replay Zipf(1.2)" if cfg.replay else "top-k softmax (renormalised)",
+                   "router_lora_rank": cfg.router_r,
+                   "lora_grads": "fp32 main_grad accumulation" if cfg.router_r else "bf16 (param dtype)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd)",
                      "achieved": round(fc1_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
@@ -244,6 +257,10 @@ def main():
         "gemm_ms_per_step": round(gemm_ms, 4),
         "bandwidth_ops_ms_per_step": round(hbm_ms, 4),
         "combine_hbm_frac": round(comb_bytes / (comb_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if comb_ms else None,
+        # routing + dispatch plan + combine (the rows are gathered inside the GEMMs,
+        # so this is the whole dispatch/combine traffic that has kernels of its own)
+        "dispatch_combine_ms_per_step": round(disp_ms, 4),
+        "dispatch_combine_gbs": round(comb_bytes / (disp_ms * 1e-3) / 1e9, 1) if disp_ms else None,
         "kernels_ms_per_step": kernels,
     }
     if not args.no_cpu_baseline:

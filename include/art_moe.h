@@ -35,7 +35,8 @@
  *   (exclusive prefix of tokens_per_expert); seg[(1+b)*(E+1) + e] for
  *   b = 0..ART_MOE_SEG_NBM-1 is the exclusive prefix over experts of
  *   ceil(count_e / BM_b) with BM_b = 64, 128, 192, 256 (row-tile schedules of the grouped
- *   GEMMs).  Build it with art_moe_dispatch_plan or art_moe_segments_from_counts.
+ *   GEMMs) and 4096 (row chunks of the segmented weight-gradient products).
+ *   Build it with art_moe_dispatch_plan or art_moe_segments_from_counts.
  */
 #ifndef ART_MOE_H
 #define ART_MOE_H
@@ -52,7 +53,7 @@ extern "C" {
 #define ART_MOE_ERR_UNSUPPORTED (-2)
 #define ART_MOE_ERR_HIP (-3)
 
-#define ART_MOE_SEG_NBM 4
+#define ART_MOE_SEG_NBM 5
 #define ART_MOE_SEG_LEN(E) ((1 + ART_MOE_SEG_NBM) * ((E) + 1))
 
 /* Library version, e.g. 100 for 0.1.0. */
@@ -208,6 +209,10 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
  * [E][Q][P].  mode: ART_MOE_WGRAD_STORE writes fp32 out, _ACCUMULATE adds to
  * fp32 out, _STORE_BF16 writes bf16 out (one rounding of the fp32 sum: the
  * parameter-dtype gradient the reference returns).
+ * M is the number of segment rows (>= seg[E]).  Segments are processed in
+ * chunks of 4096 rows; chunks of segments longer than that leave fp32
+ * partials in `workspace` (art_moe_wgrad_workspace_bytes), summed in chunk
+ * order afterwards: results do not depend on the schedule.
  * Experts with no rows get zeros (or keep out when accumulating).
  * Split output: with out2 != NULL, columns q < q_split land in out and
  * columns q >= q_split in out2 at column q - q_split (strides o2_*), e.g. the
@@ -216,11 +221,16 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
  * (cute_grouped_lora_quack.py:301-334, 411-431, 585-616). */
 int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
                           const void *r, int64_t ldr, const int32_t *r_rows,
-                          const int32_t *seg, int32_t E, int32_t P, int32_t Q,
-                          float alpha, void *out, int64_t o_es,
+                          const int32_t *seg, int32_t E, int64_t M, int32_t P,
+                          int32_t Q, float alpha, void *out, int64_t o_es,
                           int64_t o_ps, int64_t o_qs, void *out2,
                           int32_t q_split, int64_t o2_es, int64_t o2_ps,
-                          int64_t o2_qs, int32_t mode, void *stream);
+                          int64_t o2_qs, int32_t mode, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+/* Workspace bytes art_moe_grouped_wgrad needs for M segment rows (0 when
+ * M <= 4096: no segment can span two 4096-row chunks). */
+size_t art_moe_wgrad_workspace_bytes(int64_t M, int32_t E, int32_t P, int32_t Q);
 
 /* ------------------------------------------------------------ router LoRA
  * No counterpart in the reference, which puts no LoRA on the router

@@ -62,9 +62,11 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
     rc = lib.art_moe_permute(null, null, 4, 2, 12, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
-    rc = lib.art_moe_grouped_wgrad(null, 64, null, null, 64, null, null, 4, 64, 12, 1.0, null,
-                                   0, 0, 0, null, 0, 0, 0, 0, 0, null)
+    rc = lib.art_moe_grouped_wgrad(null, 64, null, null, 64, null, null, 4, 100, 64, 12, 1.0,
+                                   null, 0, 0, 0, null, 0, 0, 0, 0, 0, null, 0, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
+    assert lib.art_moe_wgrad_workspace_bytes(4096, 128, 2048, 32) == 0
+    assert lib.art_moe_wgrad_workspace_bytes(65536, 128, 2048, 32) == (16 + 128) * 2048 * 32 * 4
     rc = lib.art_moe_router_lora_grad(null, null, 8, 8, null, 512, 128, 1.0, null, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"r * E" in lib.art_moe_last_error()
 

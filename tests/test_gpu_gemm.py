@@ -156,7 +156,8 @@ def test_fc2_dgrad_swiglu(device, e, m, f, h, kt):
 
 @pytest.mark.parametrize("e,m,p,q,gather,transpose", [
     (8, 1000, 256, 16, True, False), (128, 4096, 2048, 32, False, False),
-    (16, 2000, 768, 16, False, True), (4, 300, 64, 128, True, True), (6, 500, 96, 48, False, False)])
+    (16, 2000, 768, 16, False, True), (4, 300, 64, 128, True, True), (6, 500, 96, 48, False, False),
+    (5, 21000, 264, 72, True, False), (3, 9000, 128, 128, False, True)])
 def test_grouped_wgrad(device, e, m, p, q, gather, transpose):
     ops = _ops()
     print(f"wgrad e={e} m={m} p={p} q={q}", flush=True)
@@ -184,10 +185,12 @@ def test_grouped_wgrad(device, e, m, p, q, gather, transpose):
             assert torch.count_nonzero(got[i]) == 0
 
 
-def test_grouped_wgrad_bf16_and_accumulate_modes(device):
-    """bf16 output is the fp32 result rounded once; accumulate adds to fp32 out."""
+@pytest.mark.parametrize("m", [1500, 12000])
+def test_grouped_wgrad_bf16_and_accumulate_modes(device, m):
+    """bf16 output is the fp32 result rounded once; accumulate adds to fp32 out
+    (m=12000 puts segments over several 4096-row chunks)."""
     ops = _ops()
-    e, m, p, q = 8, 1500, 320, 32
+    e, p, q = 8, 320, 32
     g = torch.Generator().manual_seed(77)
     counts = _counts(e, m, seed=5)
     lm = torch.randn(m, p, generator=g).to(torch.bfloat16).to(device)
