@@ -47,12 +47,17 @@ class FrozenExperts:
     w1  [E, 2F, H] FC1 (TE GroupedLinear ``weight{e}`` layout, gate rows first)
     w2  [E, H, F]  FC2
     w1t [E, H, 2F], w2t [E, F, H] transposed copies for the data gradients.
+    With fp8 storage (``build_fp8``) w1 / w2 and their copies hold e4m3fn
+    bytes and w1_scale [E, 2F] / w2_scale [E, H] the per-output-row scales
+    (per-k scales of the transposed copies); the products use bf16(q * s).
     """
     w_r: torch.Tensor | None
     w1: torch.Tensor
     w2: torch.Tensor
     w1t: torch.Tensor
     w2t: torch.Tensor
+    w1_scale: torch.Tensor | None = None
+    w2_scale: torch.Tensor | None = None
 
     @classmethod
     def build(cls, w_r, w1, w2) -> "FrozenExperts":
@@ -60,6 +65,19 @@ class FrozenExperts:
         w2 = w2.detach().contiguous()
         return cls(w_r.detach().contiguous() if w_r is not None else None,
                    w1, w2, ops.transposed(w1), ops.transposed(w2))
+
+    @classmethod
+    def build_fp8(cls, w_r, w1_q, w1_scale, w2_q, w2_scale) -> "FrozenExperts":
+        """From e4m3fn weights with per-output-row fp32 scales (art_amd.quant)."""
+        from ..quant import transpose_fp8
+        w1_q, w2_q = w1_q.detach().contiguous(), w2_q.detach().contiguous()
+        return cls(w_r.detach().contiguous() if w_r is not None else None, w1_q, w2_q,
+                   transpose_fp8(w1_q), transpose_fp8(w2_q),
+                   w1_scale.detach().float().contiguous(), w2_scale.detach().float().contiguous())
+
+    @property
+    def fp8(self) -> bool:
+        return self.w1_scale is not None
 
     @property
     def num_experts(self) -> int:
@@ -200,9 +218,9 @@ class _MoELoRALayerFn(torch.autograd.Function):
         rows = plan.row_token
         t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
         y1, h = ops.fc1_swiglu(x, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
-                               tl=t1, l1=l1)
+                               tl=t1, l1=l1, w1_scale=base.w1_scale)
         t2 = ops.grouped_gemm(h, a2p, plan.seg, e, m=m)
-        y2 = ops.grouped_gemm(h, base.w2, plan.seg, e, m=m, tl=t2, l=l2)
+        y2 = ops.grouped_gemm(h, base.w2, plan.seg, e, m=m, tl=t2, l=l2, b_scale=base.w2_scale)
         y = ops.combine(y2, plan.dest, t)
         ctx.save_for_backward(x, idx, w, plan.dest, rows, plan.row_prob, plan.seg, t1, y1, h, t2,
                               a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, brp, t_rb, seg1)
@@ -246,9 +264,10 @@ class _MoELoRALayerFn(torch.autograd.Function):
         # FC2 data gradient with the SwiGLU backward in its epilogue
         g2 = ops.grouped_gemm(dy, bdp, seg, e, m=m, a_rows=rows, alpha=sd)
         dy1, dp_part = ops.fc2_dgrad_swiglu(dy, base.w2t, seg, e, y1, row_prob, m=m, a_rows=rows,
-                                            tl=g2, l2=adp)
+                                            tl=g2, l2=adp, w2_scale=base.w2_scale)
         g1 = ops.grouped_gemm(dy1, gb, seg, e, m=m)
-        dx_perm = ops.grouped_gemm(dy1, base.w1t, seg, e, m=m, tl=g1, l=a1cat)
+        dx_perm = ops.grouped_gemm(dy1, base.w1t, seg, e, m=m, tl=g1, l=a1cat,
+                                   b_scale=base.w1_scale, scale_per_k=True)
         # router: softmax backward over the k selected logits
         dl, dlogits = ops.router_backward(dp_part, dest, w, idx, e,
                                           dense=ctx.logits_supplied and ctx.needs_input_grad[1])

@@ -164,17 +164,37 @@ def combine(y_perm: torch.Tensor, dest: torch.Tensor, num_tokens: int, *,
 
 
 # ------------------------------------------------------------ grouped GEMM
+FP8_DTYPES = (torch.float8_e4m3fn, torch.uint8)
+
+
+def _weight_format(b: torch.Tensor, b_scale: torch.Tensor | None, per_k: bool):
+    """(format code, scale pointer, scale expert stride) of a weight operand:
+    bf16, or fp8 e4m3fn bytes (float8_e4m3fn or uint8 view) with fp32 scales."""
+    if b.dtype == torch.bfloat16:
+        _need(b_scale is None, "bf16 weights take no scale")
+        return _lib.B_BF16, None, 0
+    _need(b.dtype in FP8_DTYPES, "weights must be bf16 or fp8 e4m3fn")
+    _need(b_scale is not None and b_scale.dtype == torch.float32 and b_scale.is_contiguous()
+          and b_scale.dim() == 2 and b_scale.shape[0] == b.shape[0],
+          "fp8 weights need contiguous fp32 scales [E, n]")
+    return (_lib.B_FP8_KSCALE if per_k else _lib.B_FP8_ROWSCALE), b_scale, b_scale.stride(0)
+
+
 def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_experts: int, *,
                  m: int | None = None, a_rows: torch.Tensor | None = None,
                  tl: torch.Tensor | None = None, l: torch.Tensor | None = None,
                  alpha: float = 1.0, out_fp32: bool = False,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, b_scale: torch.Tensor | None = None,
+                 scale_per_k: bool = False) -> torch.Tensor:
     """C = alpha * (A[row(m)] @ B[e]^T + Tl @ L[e]^T) per expert segment.
 
-    a [*, K] bf16; b [E, N, K] bf16 (last dim contiguous); tl [M, kt], l [E, N, kt].
+    a [*, K] bf16; b [E, N, K] bf16 (last dim contiguous), or fp8 e4m3fn with
+    ``b_scale`` [E, N] (per row) / [E, K] (``scale_per_k``): B = bf16(q * s);
+    tl [M, kt], l [E, N, kt].
     """
-    _cuda(a, b, seg, a_rows, tl, l)
-    _need(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16, "A and B must be bf16")
+    _cuda(a, b, seg, a_rows, tl, l, b_scale)
+    _need(a.dtype == torch.bfloat16, "A must be bf16")
+    fmt, bsc, bs_es = _weight_format(b, b_scale, scale_per_k)
     _need(b.dim() == 3 and b.shape[0] == num_experts, "B must be [E, N, K]")
     n, k = b.shape[1], b.shape[2]
     _need(a.shape[-1] == k, f"A has K={a.shape[-1]}, B has K={k}")
@@ -190,7 +210,8 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32 if out_fp32 else torch.bfloat16, device=a.device)
     call("art_moe_grouped_gemm", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(b), _rowmajor(b, "B"),
-         b.stride(0), ptr(tl), ldt, ptr(l), ldl, l_es, kt, ptr(seg), num_experts, m, n, k,
+         b.stride(0), ptr(bsc), bs_es, fmt, ptr(tl), ldt, ptr(l), ldl, l_es, kt, ptr(seg),
+         num_experts, m, n, k,
          float(alpha), ptr(out), _rowmajor(out, "C"), int(out.dtype == torch.float32),
          stream_ptr(a.device))
     return out
@@ -198,12 +219,15 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
 
 def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts: int,
                row_prob: torch.Tensor, *, m: int, a_rows: torch.Tensor | None = None,
-               tl: torch.Tensor | None = None, l1: torch.Tensor | None = None):
-    """(y1 [M,2F], h [M,F]) = FC1 (+LoRA) then weighted SwiGLU, fused."""
-    _cuda(a, w1, seg, row_prob, a_rows, tl, l1)
+               tl: torch.Tensor | None = None, l1: torch.Tensor | None = None,
+               w1_scale: torch.Tensor | None = None):
+    """(y1 [M,2F], h [M,F]) = FC1 (+LoRA) then weighted SwiGLU, fused.
+    ``w1`` is bf16, or fp8 e4m3fn with per-row scales ``w1_scale`` [E, 2F]."""
+    _cuda(a, w1, seg, row_prob, a_rows, tl, l1, w1_scale)
     e, f2, k = w1.shape
     f = f2 // 2
-    _need(w1.is_contiguous() and w1.dtype == torch.bfloat16, "w1 must be contiguous bf16 [E, 2F, K]")
+    _need(w1.is_contiguous(), "w1 must be contiguous [E, 2F, K]")
+    fmt, wsc, _ = _weight_format(w1, w1_scale, False)
     kt = 0
     ldt = 0
     if tl is not None:
@@ -212,7 +236,8 @@ def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts
         ldt = _rowmajor(tl, "Tl")
     y1 = torch.empty((m, f2), dtype=torch.bfloat16, device=a.device)
     h = torch.empty((m, f), dtype=torch.bfloat16, device=a.device)
-    call("art_moe_fc1_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w1), ptr(tl), ldt,
+    call("art_moe_fc1_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w1), ptr(wsc), fmt,
+         ptr(tl), ldt,
          ptr(l1), kt, ptr(seg), num_experts, m, f, k, ptr(row_prob), ptr(y1), ptr(h),
          stream_ptr(a.device))
     return y1, h
@@ -225,11 +250,13 @@ def dgrad_swiglu_parts(f: int) -> int:
 def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_experts: int,
                      y1: torch.Tensor, row_prob: torch.Tensor, *, m: int,
                      a_rows: torch.Tensor | None = None, tl: torch.Tensor | None = None,
-                     l2: torch.Tensor | None = None):
-    """(dy1 [M,2F] bf16, dp_part [n_parts, M] fp32) of the FC2 dgrad + SwiGLU backward."""
-    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2)
+                     l2: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None):
+    """(dy1 [M,2F] bf16, dp_part [n_parts, M] fp32) of the FC2 dgrad + SwiGLU backward.
+    ``w2t`` is bf16, or fp8 e4m3fn with the FC2 row scales ``w2_scale`` [E, K]."""
+    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2, w2_scale)
     e, f, k = w2t.shape
-    _need(w2t.is_contiguous() and w2t.dtype == torch.bfloat16, "w2t must be contiguous bf16 [E, F, K]")
+    _need(w2t.is_contiguous(), "w2t must be contiguous [E, F, K]")
+    fmt, wsc, _ = _weight_format(w2t, w2_scale, True)
     _need(y1.is_contiguous() and y1.shape == (m, 2 * f), "y1 must be contiguous [M, 2F]")
     kt = 0
     ldt = 0
@@ -239,7 +266,8 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
         ldt = _rowmajor(tl, "Tl")
     dy1 = torch.empty((m, 2 * f), dtype=torch.bfloat16, device=a.device)
     dp_part = torch.empty((dgrad_swiglu_parts(f), m), dtype=torch.float32, device=a.device)
-    call("art_moe_fc2_dgrad_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w2t), ptr(tl), ldt,
+    call("art_moe_fc2_dgrad_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w2t), ptr(wsc),
+         fmt, ptr(tl), ldt,
          ptr(l2), kt, ptr(seg), num_experts, m, f, k, ptr(y1), ptr(row_prob), ptr(dy1),
          ptr(dp_part), stream_ptr(a.device))
     return dy1, dp_part

@@ -6,8 +6,9 @@ C1  Qwen3-30B-A3B expert layer: T=8192, H=2048, E=128, k=8, F=768, r=16
 C2  C1 shapes with routing replay: Zipf(1.2) expert ids, Dirichlet(1) weights
 C3  long context: T=32768, r=64, router LoRA rank 64 (A_r [H,64], B_r [64,E]),
     LoRA gradients accumulated in fp32
-C4  wide layer: H=4096, F=1536, T=16384, r=32 (fp8 base weights upstream;
-    here bf16 base weights until the fp8 path lands)
+C4  wide layer: H=4096, F=1536, T=16384, r=32; base weights quantised to
+    e4m3fn with per-output-channel fp32 scales (amax / 448), dequantised to
+    bf16 inside the products (art_amd.quant)
 
 Inputs follow the specification: x ~ N(0,1); base weights ~ N(0, 0.02);
 LoRA A, B ~ N(0, 0.01) (B non-zero so both factors get gradients).  The
@@ -47,6 +48,7 @@ class LayerConfig:
     replay: bool = False
     note: str = ""
     router_r: int = 0       # router LoRA rank (0: none)
+    fp8: bool = False       # frozen base weights stored as e4m3fn + per-row fp32 scales
 
     @property
     def scale(self) -> float:
@@ -84,8 +86,8 @@ CONFIGS = {
                       note="C1 + Zipf(1.2) routing replay"),
     "C3": LayerConfig("C3", T=32768, H=2048, E=128, k=8, F=768, r=64, router_r=64,
                       note="long-context GRPO step, router LoRA, fp32 LoRA grad accumulation"),
-    "C4": LayerConfig("C4", T=16384, H=4096, E=128, k=8, F=1536, r=32,
-                      note="wide layer"),
+    "C4": LayerConfig("C4", T=16384, H=4096, E=128, k=8, F=1536, r=32, fp8=True,
+                      note="wide layer, fp8 e4m3fn base weights (per-output-channel scales)"),
 }
 
 

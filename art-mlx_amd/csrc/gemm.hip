@@ -42,9 +42,11 @@ struct NTArgs {
   const bf16 *a;
   int64_t lda;
   const int32_t *a_rows;
-  const bf16 *b;
+  const bf16 *b;      // bf16 [E][N][ldb], or fp8 e4m3fn bytes with b_scale
   int64_t ldb;
   int64_t b_es;
+  const float *b_scale;  // fp8 B: per-row (N) or per-k scale, expert stride bs_es
+  int64_t bs_es;
   const bf16 *t;
   int64_t ldt;
   const bf16 *l;
@@ -167,6 +169,78 @@ __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int w
   }
 }
 
+// fp8 weight tiles (W8A16 path): B rows of one 64-wide k-tile are 64 bytes,
+// moved in 1 KB DMA blocks of 16 rows; 16-byte chunk c of row r lives at
+// physical chunk c ^ swz8(r).
+enum { B_BF16 = ART_MOE_B_BF16, B_FP8_ROWSCALE = ART_MOE_B_FP8_ROWSCALE,
+       B_FP8_KSCALE = ART_MOE_B_FP8_KSCALE };
+
+__device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
+
+__device__ __forceinline__ void dma16v(const void *g, void *lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)lds, 16, 0, 0);
+}
+
+template <int A_PW, int B_PW8, int A_BYTES>
+__device__ __forceinline__ void issue_stage_b8(char *st, int wave, const char *abase,
+                                               const char *bbase, const uint32_t (&aoff)[A_PW],
+                                               const uint32_t (&boff)[B_PW8], uint32_t sh_a,
+                                               uint32_t sh_b) {
+#pragma unroll
+  for (int i = 0; i < A_PW; ++i)
+    dma16((const bf16 *)(abase + (aoff[i] + sh_a)), st + (wave * A_PW + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < B_PW8; ++i)
+    dma16v(bbase + (boff[i] + sh_b), st + A_BYTES + (wave * B_PW8 + i) * 1024);
+}
+
+// Eight e4m3fn weights -> bf16(q * scale): the dequantised weight of the
+// reference path (fp8 value times its fp32 scale, rounded once to bf16).
+__device__ __forceinline__ bf16x8 dequant8(uint2 q, const float (&sc)[8]) {
+  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)q.x, false);
+  const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)q.x, true);
+  const auto c = __builtin_amdgcn_cvt_pk_f32_fp8((int)q.y, false);
+  const auto d = __builtin_amdgcn_cvt_pk_f32_fp8((int)q.y, true);
+  bf16x8 o;
+  o[0] = (bf16)(a[0] * sc[0]); o[1] = (bf16)(a[1] * sc[1]);
+  o[2] = (bf16)(b[0] * sc[2]); o[3] = (bf16)(b[1] * sc[3]);
+  o[4] = (bf16)(c[0] * sc[4]); o[5] = (bf16)(c[1] * sc[5]);
+  o[6] = (bf16)(d[0] * sc[6]); o[7] = (bf16)(d[1] * sc[7]);
+  return o;
+}
+
+// Operands of one 16-wide k step of an fp8-weight stage: A as in load_frags,
+// B dequantised from 8 bytes per lane with its row scale (forward products)
+// or the k-tile's per-k scales staged at `ksc` (data-gradient products).
+template <int TM, int TN, int WTM, int WTN, int A_BYTES, int BQ8>
+__device__ __forceinline__ void load_frags8(const char *st, int kk, int wm, int wn, int lrow, int lk,
+                                            bf16x8 (&af)[TM], bf16x8 (&bfv)[TN],
+                                            const float (&bsc)[TN], const float *ksc) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = wm * WTM + i * 32 + lrow;
+    af[i] = *(const bf16x8 *)(st + r * 128 + (((kk * 2 + lk) ^ swz(r)) << 4));
+  }
+  float kscale[8];
+  if (BQ8 == B_FP8_KSCALE) {
+    const float4 k0 = *(const float4 *)(ksc + kk * 16 + lk * 8);
+    const float4 k1 = *(const float4 *)(ksc + kk * 16 + lk * 8 + 4);
+    kscale[0] = k0.x; kscale[1] = k0.y; kscale[2] = k0.z; kscale[3] = k0.w;
+    kscale[4] = k1.x; kscale[5] = k1.y; kscale[6] = k1.z; kscale[7] = k1.w;
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int r = wn * WTN + j * 32 + lrow;
+    const uint2 q = *(const uint2 *)(st + A_BYTES + r * 64 + ((kk ^ swz8(r)) << 4) + lk * 8);
+    if (BQ8 == B_FP8_KSCALE) {
+      bfv[j] = dequant8(q, kscale);
+    } else {
+      const float rs[8] = {bsc[j], bsc[j], bsc[j], bsc[j], bsc[j], bsc[j], bsc[j], bsc[j]};
+      bfv[j] = dequant8(q, rs);
+    }
+  }
+}
+
 // B is the MFMA's first operand: acc[i][j] accumulates the transposed block,
 // so each lane ends up with 4 consecutive output columns of one row.
 template <int TM, int TN>
@@ -179,16 +253,21 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&a
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfv[j], af[i], acc[i][j], 0, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int EPI>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int BK = 64;
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
-  constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  constexpr int KSC_BYTES = BQ8 == B_FP8_KSCALE ? BK * 4 : 0;  // per-k scales of an fp8 k-tile
+  constexpr int STAGE_BYTES = A_BYTES + B_BYTES + KSC_BYTES;
   constexpr int A_PW = BM / 8 / NW, B_PW = BN / 8 / NW;  // 1 KB DMA blocks per wave
-  constexpr int G = A_PW + B_PW;                          // DMA instructions per stage per wave
+  constexpr int B_PW8 = BQ8 ? BN / 16 / NW : 1;           // fp8 B: 16 rows per 1 KB block
+  // DMA instructions per stage per wave.  With fp8 weights the base stages
+  // issue fewer than the LoRA stages; waiting with the smaller count is
+  // conservative for both (the per-k scale DMA of wave 0 likewise).
+  constexpr int G = BQ8 ? A_PW + B_PW8 : A_PW + B_PW;
   constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
   constexpr int UMASK = (BN / 4 >= 32) ? 31 : (BN / 4 - 1);  // staging swizzle (8-byte units)
   static_assert(TM >= 1 && TN >= 1 && A_PW >= 1 && B_PW >= 1, "tile config");
@@ -197,6 +276,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   static_assert(BM * BN * 2 <= LDS_BYTES, "epilogue staging must fit the LDS ring");
   static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 4, "vmcnt range");
   static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
+  static_assert(!BQ8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
 
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
   __shared__ float sRed[EPI == EPI_SWIGLU_BWD ? WN * BM : 1];
@@ -230,8 +310,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // 32-bit byte offsets from wave-uniform bases (the host checks that every
     // operand spans less than 4 GiB).
     const char *abase = (const char *)p.a;
-    const char *bbase = (const char *)(p.b + (int64_t)e * p.b_es);
-    uint32_t aoff[A_PW], boff[B_PW];
+    const char *bbase = BQ8 ? (const char *)p.b + (int64_t)e * p.b_es
+                            : (const char *)(p.b + (int64_t)e * p.b_es);
+    uint32_t aoff[A_PW], boff[BQ8 ? B_PW8 : B_PW];
 #pragma unroll
     for (int i = 0; i < A_PW; ++i) {
       int m = m0 + (wave * A_PW + i) * 8 + drow;
@@ -240,12 +321,31 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * A_PW + i) * 8 + drow));
       aoff[i] = (src * (uint32_t)p.lda + ch * 8) * 2u;
     }
+    if (BQ8) {
 #pragma unroll
-    for (int i = 0; i < B_PW; ++i) {
-      const int r = (wave * B_PW + i) * 8 + drow;
-      const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
-      const uint32_t ch = (uint32_t)((lane & 7) ^ swz(r));
-      boff[i] = ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
+      for (int i = 0; i < B_PW8; ++i) {
+        const int r = (wave * B_PW8 + i) * 16 + (lane >> 2);
+        const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
+        const uint32_t ch = (uint32_t)((lane & 3) ^ swz8(r));
+        boff[i] = (uint32_t)n * (uint32_t)p.ldb + ch * 16u;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_PW; ++i) {
+        const int r = (wave * B_PW + i) * 8 + drow;
+        const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
+        const uint32_t ch = (uint32_t)((lane & 7) ^ swz(r));
+        boff[i] = ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
+      }
+    }
+    // fp8 weights with row scales: the scale of each B fragment row
+    float bsc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      bsc[j] = 1.0f;
+      if (BQ8 == B_FP8_ROWSCALE)
+        bsc[j] = p.b_scale[(int64_t)e * p.bs_es +
+                           b_source_row<EPI, BN>(wn * WTN + j * 32 + lrow, nt, p.N, p.F)];
     }
 
     // LoRA K-extension stages: offsets into Tl (same rows, not gathered) and L,
@@ -274,14 +374,24 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #define ART_ISSUE(ks)                                                                         \
   do {                                                                                        \
     char *st_ = smem + ((ks) % STAGES) * STAGE_BYTES;                                         \
-    if ((ks) < nk_full)                                                                       \
-      issue_stage<A_PW, B_PW, A_BYTES>(st_, wave, abase, bbase, aoff, boff,                   \
-                                       (uint32_t)((ks) * BK * 2));                            \
-    else if ((ks) < nk_main)                                                                  \
-      issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, abase, bbase, aoff, boff,        \
-                                            (ks) * BK, p.K);                                  \
-    else                                                                                      \
+    if ((ks) < nk_full) {                                                                     \
+      if constexpr (BQ8 != B_BF16) {                                                          \
+        issue_stage_b8<A_PW, B_PW8, A_BYTES>(st_, wave, abase, bbase, aoff, boff,             \
+                                             (uint32_t)((ks) * BK * 2), (uint32_t)((ks) * BK)); \
+        if (BQ8 == B_FP8_KSCALE && wave == 0 && lane < BK / 4)                                \
+          dma16v(p.b_scale + (int64_t)e * p.bs_es + (ks) * BK + lane * 4,                     \
+                 st_ + A_BYTES + B_BYTES);                                                    \
+      } else {                                                                                \
+        issue_stage<A_PW, B_PW, A_BYTES>(st_, wave, abase, bbase, aoff, boff,                 \
+                                         (uint32_t)((ks) * BK * 2));                          \
+      }                                                                                       \
+    } else if ((ks) < nk_main) {                                                              \
+      if constexpr (BQ8 == B_BF16)                                                            \
+        issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, abase, bbase, aoff, boff,      \
+                                              (ks) * BK, p.K);                                \
+    } else {                                                                                  \
       ART_ISSUE_LORA(ks);                                                                     \
+    }                                                                                         \
   } while (0)
 
     f32x16 acc[TM][TN];
@@ -316,12 +426,22 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       ART_STAGE_IN(ks);
       const char *st = smem + (ks % STAGES) * STAGE_BYTES;
       bf16x8 af0[TM], bf0[TN], af1[TM], bf1[TN];
-      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
-      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1);
-      mma_step<TM, TN>(acc, af0, bf0);
-      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
-      mma_step<TM, TN>(acc, af1, bf1);
-      load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
+      if (BQ8) {
+        const float *ksc = (const float *)(st + A_BYTES + B_BYTES);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 0, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 1, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
+        mma_step<TM, TN>(acc, af0, bf0);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 2, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
+        mma_step<TM, TN>(acc, af1, bf1);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 3, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
+      } else {
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1);
+        mma_step<TM, TN>(acc, af0, bf0);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
+        mma_step<TM, TN>(acc, af1, bf1);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
+      }
       mma_step<TM, TN>(acc, af0, bf0);
       mma_step<TM, TN>(acc, af1, bf1);
     }
@@ -542,7 +662,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int EPI>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
                      const char *what) {
   constexpr int bmi = BM / 64 - 1;  // segment-table row of this tile height
@@ -553,7 +673,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   if (occ == 0) {
     int o = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI>, NT, 0) != hipSuccess || o < 1)
+            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8>, NT, 0) != hipSuccess || o < 1)
       o = 1;
     occ = o;
   }
@@ -566,7 +686,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   if (grid > max_tiles) grid = max_tiles;
   if (grid >= 8) grid &= ~(int64_t)7;
   if (grid < 1) grid = 1;
-  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI><<<dim3((unsigned)grid), NT, 0, s>>>(p);
+  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8><<<dim3((unsigned)grid), NT, 0, s>>>(p);
   return check_launch(what);
 }
 
@@ -595,6 +715,18 @@ static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, h
     case 9: return launch_nt<192, 128, 2, 2, 3, EPI>(p, seg, M, s, what);
     default: return launch_nt<256, 256, 2, 2, 2, EPI>(p, seg, M, s, what);
   }
+}
+
+// fp8-weight products: one macro tile per epilogue (the defaults above).
+template <int EPI>
+static int launch_fp8(int fmt, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
+                      const char *what) {
+  if (EPI == EPI_SWIGLU_BWD) {
+    if (fmt == B_FP8_ROWSCALE) return launch_nt<192, 256, 2, 4, 2, EPI, B_FP8_ROWSCALE>(p, seg, M, s, what);
+    return launch_nt<192, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
+  }
+  if (fmt == B_FP8_ROWSCALE) return launch_nt<256, 256, 2, 4, 2, EPI, B_FP8_ROWSCALE>(p, seg, M, s, what);
+  return launch_nt<256, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
 }
 
 static int tile_cfg(int dflt) {
@@ -639,14 +771,34 @@ static int check_common(const void *a, int64_t lda, const void *b, int64_t ldb,
   return ART_MOE_OK;
 }
 
+// fp8 weights: 64-wide k-tiles only (no partial k-tile), 16-byte rows and
+// scale rows (the per-k scales move in 16-byte chunks).
+static int check_fp8(int32_t fmt, const void *b, int64_t ldb, const float *b_scale,
+                     int64_t bs_es, int32_t K, int32_t N, const char *who) {
+  ART_REQUIRE(fmt == ART_MOE_B_BF16 || fmt == ART_MOE_B_FP8_ROWSCALE || fmt == ART_MOE_B_FP8_KSCALE,
+              "%s: unknown weight format %d", who, fmt);
+  if (fmt == ART_MOE_B_BF16) return ART_MOE_OK;
+  ART_REQUIRE(K % 64 == 0, "%s: fp8 weights need K a multiple of 64 (K=%d)", who, K);
+  ART_REQUIRE(ldb % 16 == 0, "%s: fp8 weights need ldb a multiple of 16", who);
+  ART_REQUIRE(b_scale && aligned16(b_scale) && bs_es % 4 == 0,
+              "%s: fp8 weights need 16-byte aligned scales with an expert stride %% 4 == 0", who);
+  ART_REQUIRE(bs_es >= (fmt == ART_MOE_B_FP8_ROWSCALE ? N : K),
+              "%s: scale expert stride too small", who);
+  (void)b;
+  return ART_MOE_OK;
+}
+
 extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
                                     const void *b, int64_t ldb, int64_t b_estride,
+                                    const float *b_scale, int64_t bs_estride, int32_t b_format,
                                     const void *tl, int64_t ldt, const void *l, int64_t ldl,
                                     int64_t l_estride, int32_t kt, const int32_t *seg, int32_t E,
                                     int64_t M, int32_t N, int32_t K, float alpha, void *c,
                                     int64_t ldc, int32_t c_fp32, void *stream) {
   clear_error();
   int rc = check_common(a, lda, b, ldb, seg, E, M, K, kt, tl, ldt, l, ldl, "grouped_gemm");
+  if (rc) return rc;
+  rc = check_fp8(b_format, b, ldb, b_scale, bs_estride, K, N, "grouped_gemm");
   if (rc) return rc;
   ART_REQUIRE(N > 0 && N % 8 == 0 && c, "grouped_gemm: need N a positive multiple of 8 and an output");
   ART_REQUIRE(ldc >= N && ldc % 8 == 0 && aligned16(c),
@@ -657,10 +809,12 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
   p.b = (const bf16 *)b; p.ldb = ldb; p.b_es = b_estride;
+  p.b_scale = b_scale; p.bs_es = bs_estride;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
   p.l = kt ? (const bf16 *)l : nullptr; p.ldl = ldl; p.l_es = l_estride; p.kt = kt;
   p.E = E; p.N = N; p.K = K; p.alpha = alpha; p.c = c; p.ldc = ldc; p.c_fp32 = c_fp32; p.M = M;
   hipStream_t s = as_stream(stream);
+  if (b_format != ART_MOE_B_BF16) return launch_fp8<EPI_STORE>(b_format, p, seg, M, s, "grouped_gemm/fp8");
   if (N <= 32) return launch_nt<128, 32, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n32");
   if (N <= 64) return launch_nt<128, 64, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n64");
   if (N <= 128) return launch_nt<128, 128, 2, 2, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n128");
@@ -668,12 +822,16 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
 }
 
 extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                                  const void *w1, const void *tl, int64_t ldt, const void *l1,
+                                  const void *w1, const float *w1_scale, int32_t w1_format,
+                                  const void *tl, int64_t ldt, const void *l1,
                                   int32_t kt, const int32_t *seg, int32_t E, int64_t M, int32_t F,
                                   int32_t K, const float *row_prob, void *y1, void *h,
                                   void *stream) {
   clear_error();
   int rc = check_common(a, lda, w1, K, seg, E, M, K, kt, tl, ldt, l1, kt, "fc1_swiglu");
+  if (rc) return rc;
+  ART_REQUIRE(w1_format != ART_MOE_B_FP8_KSCALE, "fc1_swiglu: fp8 W1 takes per-row scales");
+  rc = check_fp8(w1_format, w1, K, w1_scale, 2 * (int64_t)F, K, 2 * F, "fc1_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 64 == 0, "fc1_swiglu: F must be a positive multiple of 64 (F=%d)", F);
   ART_REQUIRE(row_prob && y1 && h, "fc1_swiglu: null pointer");
@@ -682,10 +840,13 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
   p.b = (const bf16 *)w1; p.ldb = K; p.b_es = (int64_t)2 * F * K;
+  p.b_scale = w1_scale; p.bs_es = (int64_t)2 * F;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
   p.l = kt ? (const bf16 *)l1 : nullptr; p.ldl = kt; p.l_es = (int64_t)2 * F * kt; p.kt = kt;
   p.E = E; p.N = 2 * F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;
   p.y1 = (bf16 *)y1; p.h = (bf16 *)h; p.M = M;
+  if (w1_format != ART_MOE_B_BF16)
+    return launch_fp8<EPI_SWIGLU_FWD>(w1_format, p, seg, M, as_stream(stream), "fc1_swiglu/fp8");
   return launch_big<EPI_SWIGLU_FWD>(tile_cfg(kTileSwigluFwd), p, seg, M, as_stream(stream),
                                     "fc1_swiglu");
 }
@@ -693,13 +854,18 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
 extern "C" int art_moe_dgrad_swiglu_parts(int32_t F) { return F > 0 ? (F + 127) / 128 : 0; }
 
 extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                                        const void *w2t, const void *tl, int64_t ldt,
+                                        const void *w2t, const float *w2_scale, int32_t w2_format,
+                                        const void *tl, int64_t ldt,
                                         const void *l2, int32_t kt, const int32_t *seg, int32_t E,
                                         int64_t M, int32_t F, int32_t K, const void *y1,
                                         const float *row_prob, void *dy1, float *dp_part,
                                         void *stream) {
   clear_error();
   int rc = check_common(a, lda, w2t, K, seg, E, M, K, kt, tl, ldt, l2, kt, "fc2_dgrad_swiglu");
+  if (rc) return rc;
+  ART_REQUIRE(w2_format != ART_MOE_B_FP8_ROWSCALE,
+              "fc2_dgrad_swiglu: fp8 W2^T takes per-k scales (the FC2 output channels)");
+  rc = check_fp8(w2_format, w2t, K, w2_scale, K, K, F, "fc2_dgrad_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 8 == 0, "fc2_dgrad_swiglu: F must be a positive multiple of 8 (F=%d)", F);
   ART_REQUIRE(y1 && row_prob && dy1 && dp_part, "fc2_dgrad_swiglu: null pointer");
@@ -708,10 +874,14 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
   p.b = (const bf16 *)w2t; p.ldb = K; p.b_es = (int64_t)F * K;
+  p.b_scale = w2_scale; p.bs_es = K;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
   p.l = kt ? (const bf16 *)l2 : nullptr; p.ldl = kt; p.l_es = (int64_t)F * kt; p.kt = kt;
   p.E = E; p.N = F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;
   p.y1_in = (const bf16 *)y1; p.dy1 = (bf16 *)dy1; p.dp_part = dp_part; p.M = M;
+  if (w2_format != ART_MOE_B_BF16)
+    return launch_fp8<EPI_SWIGLU_BWD>(w2_format, p, seg, M, as_stream(stream),
+                                      "fc2_dgrad_swiglu/fp8");
   return launch_big<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwd), p, seg, M, as_stream(stream),
                                     "fc2_dgrad_swiglu");
 }

@@ -218,8 +218,8 @@ __global__ __launch_bounds__(1024) void segments_kernel(const CT *__restrict__ c
     if (b == 0) {
       v = c;
     } else {
-      // row-tile heights 64, 128, 192, 256 and the 4096-row wgrad chunk
-      const int bm = b == ART_MOE_SEG_NBM ? 4096 : 64 * b;
+      // row-tile heights 64, 128, 192, 256 and the 2048-row wgrad chunk
+      const int bm = b == ART_MOE_SEG_NBM ? 2048 : 64 * b;
       v = (c + bm - 1) / bm;
     }
     int total;

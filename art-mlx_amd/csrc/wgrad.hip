@@ -31,7 +31,7 @@ namespace art {
 
 constexpr int kWgBK = 64;          // segment rows per main-loop step
 constexpr int kWgBP = 128;         // P extent of a workgroup tile
-constexpr int kWgChunkRows = 4096; // rows per chunk: BM of the segment table's last tile row
+constexpr int kWgChunkRows = 2048; // rows per chunk: BM of the segment table's last tile row
 constexpr int kWgChunkSegRow = ART_MOE_SEG_NBM;  // that row's index in the table
 
 struct WArgs {
@@ -130,8 +130,15 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
   constexpr int BUF = (kWgBP + BQ) * 128;                         // bytes per LDS buffer
   __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
 
+  // 1-D grid, XCD-aware: workgroups are dispatched round-robin over the 8
+  // XCDs, so the tiles of chunk c all go to XCD c % 8, back to back, and
+  // share its L2 for the chunk's rows.
+  const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int per_chunk = a.n_pt * a.n_qt;
+  const int c = (j / per_chunk) * 8 + xcd;
+  const int tile = j - (j / per_chunk) * per_chunk;
+  const int ty = tile % a.n_pt, tz = tile / a.n_pt;
   const int32_t *cpre = a.seg + kWgChunkSegRow * (a.E + 1);
-  const int c = blockIdx.x;
   if (c >= cpre[a.E]) return;  // workgroup-uniform
   int lo = 0, hi = a.E - 1;    // expert of chunk c: the last e with cpre[e] <= c
   while (lo < hi) {
@@ -142,7 +149,7 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
   const int nce = cpre[e + 1] - cpre[e];
   const int m0 = a.seg[e] + (c - cpre[e]) * kWgChunkRows;
   const int m1 = min(a.seg[e + 1], m0 + kWgChunkRows);
-  const int p0 = blockIdx.y * kWgBP, q0 = blockIdx.z * BQ;
+  const int p0 = ty * kWgBP, q0 = tz * BQ;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wp = wave % WP, wq = wave / WP;
   const int l16 = lane & 15, g4 = lane >> 4;
@@ -200,7 +207,7 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
   // the host sized nothing for it, so nothing is written)
   if (nce != 1 && a.ws == nullptr) return;
   float *part = nce == 1 ? nullptr
-      : a.ws + (((size_t)c * a.n_pt + blockIdx.y) * a.n_qt + blockIdx.z) * (size_t)(kWgBP * BQ);
+      : a.ws + (((size_t)c * a.n_pt + ty) * a.n_qt + tz) * (size_t)(kWgBP * BQ);
 #pragma unroll
   for (int i = 0; i < TP; ++i)
 #pragma unroll
@@ -249,8 +256,10 @@ static int launch_wgrad(WArgs a, int64_t M, hipStream_t s) {
   a.n_pt = (a.P + kWgBP - 1) / kWgBP;
   a.n_qt = (a.Q + BQ - 1) / BQ;
   if (M > 0) {
-    wgrad_kernel<BQ, WP, WQ, TP, TQ>
-        <<<dim3((unsigned)wgrad_max_chunks(M, a.E), a.n_pt, a.n_qt), 256, 0, s>>>(a);
+    const int64_t groups = (wgrad_max_chunks(M, a.E) + 7) / 8;  // chunk groups of 8 (one per XCD)
+    const int64_t blocks = groups * 8 * a.n_pt * a.n_qt;
+    ART_REQUIRE(blocks < (int64_t)1 << 31, "grouped_wgrad: too many tiles");
+    wgrad_kernel<BQ, WP, WQ, TP, TQ><<<dim3((unsigned)blocks), 256, 0, s>>>(a);
     if (int rc = check_launch("grouped_wgrad")) return rc;
   }
   wgrad_reduce_kernel<BQ><<<dim3((unsigned)a.E, a.n_pt, a.n_qt), 256, 0, s>>>(a);

@@ -89,7 +89,14 @@ def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0):
 
     dev = torch.device("cuda:0")
     inp = make_inputs(cfg, dev, seed=seed)
-    base = moe_layer.FrozenExperts.build(inp.w_r, inp.w1, inp.w2)
+    if cfg.fp8:
+        from art_amd.quant import quantize_fp8_rows
+        q1, s1 = quantize_fp8_rows(inp.w1)
+        q2, s2 = quantize_fp8_rows(inp.w2)
+        inp.w1 = inp.w2 = None
+        base = moe_layer.FrozenExperts.build_fp8(inp.w_r, q1, s1, q2, s2)
+    else:
+        base = moe_layer.FrozenExperts.build(inp.w_r, inp.w1, inp.w2)
     names = NAMES + (("a_r", "b_r") if cfg.router_r else ())
     lora = {n: inp.lora[n].requires_grad_() for n in names}
     fuse = bool(cfg.router_r)   # C3: LoRA gradients accumulate in fp32 main_grad
@@ -137,6 +144,10 @@ def cpu_baseline(cfg, tokens: int, iters: int, seed: int = 0):
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     inp = make_inputs(cfg, "cpu", seed=seed, T=tokens, dtype=torch.float32)
+    if cfg.fp8:   # the reference path computes with the dequantised weights
+        from art_amd.quant import dequantize_fp8_rows, quantize_fp8_rows
+        inp.w1 = dequantize_fp8_rows(*quantize_fp8_rows(inp.w1)).float()
+        inp.w2 = dequantize_fp8_rows(*quantize_fp8_rows(inp.w2)).float()
     names = NAMES + (("a_r", "b_r") if cfg.router_r else ())
     leaves = {n: inp.lora[n].requires_grad_() for n in names}
     s = cfg.scale
@@ -246,6 +257,8 @@ def main():
                    "E": cfg.E, "k": cfg.k, "F": f, "r": r, "alpha": cfg.alpha,
                    "routing": "replay Zipf(1.2)" if cfg.replay else "top-k softmax (renormalised)",
                    "router_lora_rank": cfg.router_r,
+                   "base_weights": ("fp8 e4m3fn + per-row fp32 scale, dequantised to bf16 in the "
+                                    "product (bf16 MFMA)") if cfg.fp8 else "bf16",
                    "lora_grads": "fp32 main_grad accumulation" if cfg.router_r else "bf16 (param dtype)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd)",

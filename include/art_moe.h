@@ -35,7 +35,7 @@
  *   (exclusive prefix of tokens_per_expert); seg[(1+b)*(E+1) + e] for
  *   b = 0..ART_MOE_SEG_NBM-1 is the exclusive prefix over experts of
  *   ceil(count_e / BM_b) with BM_b = 64, 128, 192, 256 (row-tile schedules of the grouped
- *   GEMMs) and 4096 (row chunks of the segmented weight-gradient products).
+ *   GEMMs) and 2048 (row chunks of the segmented weight-gradient products).
  *   Build it with art_moe_dispatch_plan or art_moe_segments_from_counts.
  */
 #ifndef ART_MOE_H
@@ -54,6 +54,12 @@ extern "C" {
 #define ART_MOE_ERR_HIP (-3)
 
 #define ART_MOE_SEG_NBM 5
+
+/* Weight storage of the grouped products (b_format / w*_format arguments):
+ * bf16, or OCP fp8 e4m3fn with an fp32 scale per output row or per k. */
+#define ART_MOE_B_BF16 0
+#define ART_MOE_B_FP8_ROWSCALE 1
+#define ART_MOE_B_FP8_KSCALE 2
 #define ART_MOE_SEG_LEN(E) ((1 + ART_MOE_SEG_NBM) * ((E) + 1))
 
 /* Library version, e.g. 100 for 0.1.0. */
@@ -152,12 +158,18 @@ int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
  * 16-byte aligned; rows are addressed with 32-bit byte offsets, so A rows
  * (source rows below M), Tl and one expert's B / L each span < 4 GiB.
  * Rows of C outside every segment are not written.
+ * b_format selects the weight storage (ART_MOE_B_*): bf16, or fp8 e4m3fn
+ * bytes with fp32 scales b_scale[e * bs_estride + i], i = n (per output row,
+ * ROWSCALE) or i = c (per k, KSCALE); the product uses bf16(q * scale) as
+ * the weight, i.e. the dequantised weight.  fp8 needs K % 64 == 0,
+ * ldb % 16 == 0 and 16-byte aligned scales with bs_estride % 4 == 0.
  * Replaces: TE GroupedLinear forward/dgrad (lora.py:1515-1521, 1559-1565),
  * QuACK varlen-M GEMMs (cute_grouped_lora_quack.py:257-298) and the
  * base + adapter add (lora.py:1529, 1571). */
 int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
                          const void *b, int64_t ldb, int64_t b_estride,
-                         const void *tl, int64_t ldt, const void *l,
+                         const float *b_scale, int64_t bs_estride,
+                         int32_t b_format, const void *tl, int64_t ldt, const void *l,
                          int64_t ldl, int64_t l_estride, int32_t kt,
                          const int32_t *seg, int32_t E, int64_t M, int32_t N,
                          int32_t K, float alpha, void *c, int64_t ldc,
@@ -168,10 +180,13 @@ int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
  * writes y1 (bf16 [M][2F], gate columns first) and
  * h[m, f] = silu(g) * u * row_prob[m] (bf16 [M][F]) where g = y1[m, f],
  * u = y1[m, F + f] rounded to bf16 first.  F % 64 == 0.
+ * W1 is bf16 (w1_format ART_MOE_B_BF16) or fp8 with per-row scales
+ * w1_scale [E][2F] (ART_MOE_B_FP8_ROWSCALE).
  * Replaces: MLPExpertsLinearFC1LoRA.forward (lora.py:1512-1529) followed by
  * weighted_bias_swiglu_impl (compile_workarounds.py:73-106). */
 int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                       const void *w1, const void *tl, int64_t ldt,
+                       const void *w1, const float *w1_scale, int32_t w1_format,
+                       const void *tl, int64_t ldt,
                        const void *l1, int32_t kt, const int32_t *seg,
                        int32_t E, int64_t M, int32_t F, int32_t K,
                        const float *row_prob, void *y1, void *h, void *stream);
@@ -187,10 +202,13 @@ int art_moe_dgrad_swiglu_parts(int32_t F);
  *   dy1[m, F + f] = dh * p * silu(g)
  *   dp_part[i][m] = partial sums over f of dh * silu(g) * u
  *                   (i < art_moe_dgrad_swiglu_parts(F)).
+ * W2T is bf16 (ART_MOE_B_BF16) or fp8 with the FC2 weight's per-output-row
+ * scales w2_scale [E][K], which are per-k scales here (ART_MOE_B_FP8_KSCALE).
  * Replaces: TE GroupedLinear dgrad of FC2 + QuACK LoRA dgrad
  * (cute_grouped_lora_quack.py:394-410) + weighted_swiglu_back. */
 int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                             const void *w2t, const void *tl, int64_t ldt,
+                             const void *w2t, const float *w2_scale,
+                             int32_t w2_format, const void *tl, int64_t ldt,
                              const void *l2, int32_t kt, const int32_t *seg,
                              int32_t E, int64_t M, int32_t F, int32_t K,
                              const void *y1, const float *row_prob, void *dy1,
@@ -210,7 +228,7 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
  * fp32 out, _STORE_BF16 writes bf16 out (one rounding of the fp32 sum: the
  * parameter-dtype gradient the reference returns).
  * M is the number of segment rows (>= seg[E]).  Segments are processed in
- * chunks of 4096 rows; chunks of segments longer than that leave fp32
+ * chunks of 2048 rows; chunks of segments longer than that leave fp32
  * partials in `workspace` (art_moe_wgrad_workspace_bytes), summed in chunk
  * order afterwards: results do not depend on the schedule.
  * Experts with no rows get zeros (or keep out when accumulating).
@@ -229,7 +247,7 @@ int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
                           size_t workspace_bytes, void *stream);
 
 /* Workspace bytes art_moe_grouped_wgrad needs for M segment rows (0 when
- * M <= 4096: no segment can span two 4096-row chunks). */
+ * M <= 2048: no segment can span two 2048-row chunks). */
 size_t art_moe_wgrad_workspace_bytes(int64_t M, int32_t E, int32_t P, int32_t Q);
 
 /* ------------------------------------------------------------ router LoRA

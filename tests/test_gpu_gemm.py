@@ -188,7 +188,7 @@ def test_grouped_wgrad(device, e, m, p, q, gather, transpose):
 @pytest.mark.parametrize("m", [1500, 12000])
 def test_grouped_wgrad_bf16_and_accumulate_modes(device, m):
     """bf16 output is the fp32 result rounded once; accumulate adds to fp32 out
-    (m=12000 puts segments over several 4096-row chunks)."""
+    (m=12000 puts segments over several 2048-row chunks)."""
     ops = _ops()
     e, p, q = 8, 320, 32
     g = torch.Generator().manual_seed(77)

@@ -25,7 +25,7 @@ def _ops():
 def _seg_expect(counts, e):
     counts = np.asarray(counts, dtype=np.int64)
     rows = [np.concatenate([[0], np.cumsum(counts)])]
-    for bm in (64, 128, 192, 256, 4096):
+    for bm in (64, 128, 192, 256, 2048):
         rows.append(np.concatenate([[0], np.cumsum((counts + bm - 1) // bm)]))
     return np.concatenate(rows)
 
