@@ -67,6 +67,8 @@ SIGNATURES = {
     "art_moe_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
     "art_moe_pack": (_I32, [_P, _I32, _P]),
+    "art_moe_weighted_swiglu": (_I32, [_P, _P, _I64, _I32, _P, _P]),
+    "art_moe_weighted_swiglu_back": (_I32, [_P, _P, _P, _I64, _I32, _P, _P, _P]),
     "art_moe_router_lora_apply": (_I32, [_P, _I64, _I32, _P, _I32, _F, _P, _P, _P]),
     "art_moe_router_lora_grad": (_I32, [_P, _P, _I64, _I32, _P, _I32, _I32, _F, _P, _P, _P]),
 }

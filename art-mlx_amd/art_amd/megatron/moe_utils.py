@@ -1,0 +1,176 @@
+"""megatron ``moe_utils`` surface on the HIP kernels: ``permute``,
+``unpermute`` and ``weighted_bias_swiglu_impl``.
+
+Signatures follow the reference's call sites: ``permute(tokens, routing_map,
+num_out_tokens=..., fused=..., drop_and_pad=...)[0]``
+(/root/reference/tests/integration/megatron/routing_replay/trace.py:390-398),
+``unpermute(permuted_tokens, sorted_indices, restore_shape, probs=None,
+routing_map=None, fused=False, drop_and_pad=False, pad_offsets=None)`` and
+``weighted_bias_swiglu_impl(input, bias, weights, fp8_input_store=False)``
+(src/art/megatron/runtime/bridge_runtime.py:801-900), including the
+reference's empty-input behaviour: correctly shaped zeros that stay in the
+autograd graph (bridge_runtime.py:812-823, 891-897).
+
+Order: rows are expert-major and token-ascending within an expert, the order
+megatron's mask-based permute produces (``arange(T).expand(E, T)
+.masked_select(routing_map.T)``, canonicalised in trace.py:181-232).
+Row data of bf16 hidden states (H % 8 == 0) moves through the HIP gather /
+combine kernels; other dtypes (token uids, fp32 metadata) through torch
+indexing on the same device.  Capacity dropping (``drop_and_pad=True``) is
+not supported.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+
+
+def _k_per_token(routing_map: torch.Tensor, num_out_tokens) -> int:
+    t = routing_map.shape[0]
+    if t == 0:
+        return 0
+    n = int(num_out_tokens) if num_out_tokens is not None else int(routing_map.sum().item())
+    if n % t:
+        raise ValueError("permute needs the same number of experts for every token "
+                         f"(num_out_tokens={n}, tokens={t})")
+    return n // t
+
+
+def _slots(routing_map: torch.Tensor, k: int) -> torch.Tensor:
+    """[T, k] int32 expert ids of each token's selected experts."""
+    return torch.topk(routing_map.to(torch.int8), k, dim=1, sorted=False).indices.to(torch.int32)
+
+
+def _hip_rows(x: torch.Tensor) -> bool:
+    return x.dtype == torch.bfloat16 and x.dim() == 2 and x.shape[1] % 8 == 0 and x.is_cuda
+
+
+class _PermuteFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, tokens, dest, num_rows: int):
+        ctx.save_for_backward(dest)
+        ctx.num_tokens = tokens.shape[0]
+        return ops.permute(tokens.contiguous(), dest, num_rows)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (dest,) = ctx.saved_tensors
+        return ops.combine(grad.contiguous(), dest, ctx.num_tokens), None, None
+
+
+class _UnpermuteFn(torch.autograd.Function):
+    """y[t] = sum_j wgt[t, j] * rows[dest[t, j]] (wgt None: 1)."""
+
+    @staticmethod
+    def forward(ctx, rows, dest, wgt):
+        ctx.save_for_backward(rows, dest, wgt)
+        return ops.combine(rows.contiguous(), dest, dest.shape[0], wgt=wgt)
+
+    @staticmethod
+    def backward(ctx, dy):
+        rows, dest, wgt = ctx.saved_tensors
+        dy = dy.contiguous()
+        d_rows = ops.permute(dy, dest, rows.shape[0])
+        d_wgt = None
+        if wgt is not None:
+            flat = dest.reshape(-1).long()
+            sel = rows.index_select(0, flat.clamp_min(0)).float()
+            d_wgt = (sel.view(*dest.shape, -1) * dy.float().unsqueeze(1)).sum(-1)
+            d_wgt = torch.where(dest >= 0, d_wgt, torch.zeros_like(d_wgt))
+            scale = torch.zeros(rows.shape[0], dtype=torch.float32, device=rows.device)
+            scale.index_put_((flat.clamp_min(0),), wgt.reshape(-1).float())
+            d_rows = (d_rows.float() * scale.unsqueeze(1)).to(d_rows.dtype)
+        return d_rows, None, d_wgt
+
+
+def permute(tokens: torch.Tensor, routing_map: torch.Tensor, probs: torch.Tensor | None = None,
+            num_out_tokens: int | None = None, fused: bool = False, drop_and_pad: bool = False):
+    """(permuted_tokens [M, H], permuted_probs [M] or None, sorted_indices [M] int64)."""
+    del fused
+    if drop_and_pad:
+        raise ValueError("permute: drop_and_pad (expert capacity) is not supported")
+    t, e = routing_map.shape
+    k = _k_per_token(routing_map, num_out_tokens)
+    if t == 0 or k == 0:
+        empty = tokens.new_zeros((0, *tokens.shape[1:]))
+        return (tokens.sum() * 0 + empty if tokens.is_floating_point() else empty,
+                None if probs is None else probs.new_zeros((0,)),
+                torch.zeros(0, dtype=torch.int64, device=tokens.device))
+    idx = _slots(routing_map, k)
+    w = probs.gather(1, idx.long()).float() if probs is not None else None
+    plan = ops.dispatch_plan(idx, w, e)
+    m = t * k
+    sorted_indices = plan.row_token[:m].long()
+    if _hip_rows(tokens):
+        out = _PermuteFn.apply(tokens, plan.dest, m)
+    else:
+        out = tokens.index_select(0, sorted_indices)
+    permuted_probs = None
+    if probs is not None:
+        permuted_probs = probs.t().contiguous().masked_select(routing_map.t().contiguous())
+    return out, permuted_probs, sorted_indices
+
+
+def unpermute(permuted_tokens: torch.Tensor, sorted_indices: torch.Tensor, restore_shape,
+              probs: torch.Tensor | None = None, routing_map: torch.Tensor | None = None,
+              fused: bool = False, drop_and_pad: bool = False,
+              pad_offsets: torch.Tensor | None = None) -> torch.Tensor:
+    """Scatter-add the permuted rows back to their tokens (weighted by ``probs``
+    [T, E] at the routed positions when given)."""
+    del fused, pad_offsets
+    if drop_and_pad:
+        raise ValueError("unpermute: drop_and_pad (expert capacity) is not supported")
+    shape = tuple(int(d) for d in restore_shape)
+    if permuted_tokens.numel() == 0:
+        zero = permuted_tokens.sum() * 0.0 + sorted_indices.sum().to(permuted_tokens) * 0.0
+        if probs is not None:
+            zero = zero + probs.to(permuted_tokens.dtype).sum() * 0.0
+        return zero.expand(shape).clone()
+    t = shape[0]
+    m = sorted_indices.numel()
+    if m % t:
+        raise ValueError("unpermute needs the same number of rows for every token")
+    k = m // t
+    # rows of each token, in permuted order: the k slots of token t
+    dest = torch.argsort(sorted_indices, stable=True).to(torch.int32).view(t, k)
+    wgt = None
+    if probs is not None:
+        if routing_map is None:
+            raise ValueError("unpermute with probs needs the routing_map")
+        permuted_probs = probs.t().contiguous().masked_select(routing_map.t().contiguous())
+        wgt = permuted_probs.float().index_select(0, dest.reshape(-1).long()).view(t, k)
+    if _hip_rows(permuted_tokens):
+        return _UnpermuteFn.apply(permuted_tokens, dest, wgt).view(shape)
+    rows = permuted_tokens if wgt is None else permuted_tokens * permuted_probs.unsqueeze(-1).to(
+        permuted_tokens.dtype)
+    out = permuted_tokens.new_zeros((t, *permuted_tokens.shape[1:]))
+    return out.index_add(0, sorted_indices, rows).view(shape)
+
+
+class _WeightedSwiGLUFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, y1, weights):
+        ctx.save_for_backward(y1, weights)
+        return ops.weighted_swiglu(y1, weights)
+
+    @staticmethod
+    def backward(ctx, dh):
+        y1, weights = ctx.saved_tensors
+        dy1, dprob = ops.weighted_swiglu_back(dh, y1, weights)
+        return dy1, dprob.view(weights.shape).to(weights.dtype)
+
+
+def weighted_bias_swiglu_impl(input: torch.Tensor, bias: torch.Tensor | None,
+                              weights: torch.Tensor, fp8_input_store: bool = False) -> torch.Tensor:
+    """``silu(gate) * up * weights`` over the two halves of ``input`` [M, 2F]
+    (gate first); ``weights`` [M] or [M, 1] (per-row routing probabilities)."""
+    del fp8_input_store   # the saved input stays bf16 here
+    if bias is not None:
+        raise ValueError("weighted_bias_swiglu_impl: bias is not supported (ART's experts have none)")
+    out_shape = (*input.shape[:-1], int(input.shape[-1]) // 2)
+    if input.numel() == 0:
+        zero = input.sum() * 0.0 + weights.to(input.dtype).sum() * 0.0
+        return zero.expand(out_shape).clone()
+    y1 = input.reshape(-1, input.shape[-1])
+    return _WeightedSwiGLUFn.apply(y1, weights.reshape(-1).float()).view(out_shape)

@@ -398,3 +398,30 @@ def router_lora_grad(dl: torch.Tensor, idx: torch.Tensor, b_t: torch.Tensor, sca
     call("art_moe_router_lora_grad", ptr(dl.contiguous()), ptr(idx.contiguous()), t, k,
          ptr(b_t.contiguous()), r, e, float(scale), ptr(g), ptr(dlog), stream_ptr(dl.device))
     return g, dlog
+
+
+# ---------------------------------------------------------- weighted SwiGLU
+def weighted_swiglu(y1: torch.Tensor, prob: torch.Tensor | None) -> torch.Tensor:
+    """h = silu(g) * u * prob (g, u = the two halves of y1 [M, 2F])."""
+    _cuda(y1, prob)
+    _need(y1.dtype == torch.bfloat16 and y1.dim() == 2 and y1.shape[1] % 16 == 0,
+          "y1 must be bf16 [M, 2F] with F % 8 == 0")
+    y1 = y1.contiguous()
+    m, f = y1.shape[0], y1.shape[1] // 2
+    h = torch.empty((m, f), dtype=torch.bfloat16, device=y1.device)
+    pr = prob.reshape(-1).float().contiguous() if prob is not None else None
+    call("art_moe_weighted_swiglu", ptr(y1), ptr(pr), m, f, ptr(h), stream_ptr(y1.device))
+    return h
+
+
+def weighted_swiglu_back(dh: torch.Tensor, y1: torch.Tensor, prob: torch.Tensor | None):
+    """(dy1 [M, 2F] bf16, dprob [M] fp32) of ``weighted_swiglu``."""
+    _cuda(dh, y1, prob)
+    y1, dh = y1.contiguous(), dh.to(torch.bfloat16).contiguous()
+    m, f = y1.shape[0], y1.shape[1] // 2
+    dy1 = torch.empty_like(y1)
+    dprob = torch.empty((m,), dtype=torch.float32, device=y1.device)
+    pr = prob.reshape(-1).float().contiguous() if prob is not None else None
+    call("art_moe_weighted_swiglu_back", ptr(dh), ptr(y1), ptr(pr), m, f, ptr(dy1), ptr(dprob),
+         stream_ptr(y1.device))
+    return dy1, dprob

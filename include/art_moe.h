@@ -250,6 +250,25 @@ int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
  * M <= 2048: no segment can span two 2048-row chunks). */
 size_t art_moe_wgrad_workspace_bytes(int64_t M, int32_t E, int32_t P, int32_t Q);
 
+/* --------------------------------------------------------- weighted SwiGLU
+ * Standalone forms of the SwiGLU the fused products run in their epilogues,
+ * for the module-level path.  y1 bf16 [M][2F] (gate columns first), prob fp32
+ * [M] (NULL: 1), F % 8 == 0, 16-byte aligned rows.
+ *   h[m, f] = silu(g) * u * prob[m],  g = y1[m, f], u = y1[m, F + f]
+ * Replaces: megatron weighted_bias_swiglu_impl (restated in
+ * src/art/megatron/compile_workarounds.py:73-106). */
+int art_moe_weighted_swiglu(const void *y1, const float *prob, int64_t M,
+                            int32_t F, void *h, void *stream);
+
+/*   dy1[m, f]     = dh * p * u * sig(g) * (1 + g * (1 - sig(g)))
+ *   dy1[m, F + f] = dh * p * silu(g)
+ *   dprob[m]      = sum_f dh * silu(g) * u          (dprob may be NULL)
+ * Replaces: megatron fused_bias_swiglu.weighted_swiglu_back
+ * (compile_workarounds.py:91-106). */
+int art_moe_weighted_swiglu_back(const void *dh, const void *y1, const float *prob,
+                                 int64_t M, int32_t F, void *dy1, float *dprob,
+                                 void *stream);
+
 /* ------------------------------------------------------------ router LoRA
  * No counterpart in the reference, which puts no LoRA on the router
  * (src/art/megatron/lora.py:1678-1889 wraps attention, GDN and experts only).
