@@ -426,24 +426,40 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       ART_STAGE_IN(ks);
       const char *st = smem + (ks % STAGES) * STAGE_BYTES;
       bf16x8 af0[TM], bf0[TN], af1[TM], bf1[TN];
+      // Fragment reads of step kk+1 are issued before the MFMAs of step kk;
+      // the scheduling fences keep the compiler from sinking each read to
+      // its first use (which would expose every LDS latency), so the wait
+      // before a step's MFMAs only covers the previous group of reads.
+#define ART_FENCE() __builtin_amdgcn_sched_barrier(0)
       if (BQ8) {
         const float *ksc = (const float *)(st + A_BYTES + B_BYTES);
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 0, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 1, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
+        ART_FENCE();
         mma_step<TM, TN>(acc, af0, bf0);
+        ART_FENCE();
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 2, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
+        ART_FENCE();
         mma_step<TM, TN>(acc, af1, bf1);
+        ART_FENCE();
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 3, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
       } else {
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1);
+        ART_FENCE();
         mma_step<TM, TN>(acc, af0, bf0);
+        ART_FENCE();
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
+        ART_FENCE();
         mma_step<TM, TN>(acc, af1, bf1);
+        ART_FENCE();
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
       }
+      ART_FENCE();
       mma_step<TM, TN>(acc, af0, bf0);
+      ART_FENCE();
       mma_step<TM, TN>(acc, af1, bf1);
+#undef ART_FENCE
     }
     // Tail: a partial base k-tile and the LoRA K-extension tiles.
     for (int ks = nk_full; ks < nk; ++ks) {
