@@ -711,10 +711,11 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
 // 0: 128x128 (2x2 waves, 4 stages)  1: 128x256 (2x2, 3)  2: 256x128 (2x2, 3)
 // 3: 128x256 (2x4, 3)               4: 256x128 (4x2, 3)  5: 256x256 (2x4, 2)
 // 6: 256x256 (4x2, 2)               7: 256x256 (2x2, 2: 128x128 per wave)
-// 8: 192x256 (2x4, 2)               9: 192x128 (2x2, 3)
-enum { kNumTileCfgs = 10 };
+// 8: 192x256 (2x4, 2)               9: 192x128 (2x2, 3)  10: 128x128 (2x2, 2)
+// 11: 128x256 (2x4, 2)             12: 256x128 (4x2, 2)
+enum { kNumTileCfgs = 13 };
 // Defaults from a sweep of the C1 products on MI355X.
-enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 8 };
+enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 11 };
 
 template <int EPI>
 static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
@@ -729,6 +730,9 @@ static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, h
     case 6: return launch_nt<256, 256, 4, 2, 2, EPI>(p, seg, M, s, what);
     case 8: return launch_nt<192, 256, 2, 4, 2, EPI>(p, seg, M, s, what);
     case 9: return launch_nt<192, 128, 2, 2, 3, EPI>(p, seg, M, s, what);
+    case 10: return launch_nt<128, 128, 2, 2, 2, EPI>(p, seg, M, s, what);
+    case 11: return launch_nt<128, 256, 2, 4, 2, EPI>(p, seg, M, s, what);
+    case 12: return launch_nt<256, 128, 4, 2, 2, EPI>(p, seg, M, s, what);
     default: return launch_nt<256, 256, 2, 2, 2, EPI>(p, seg, M, s, what);
   }
 }
@@ -738,8 +742,8 @@ template <int EPI>
 static int launch_fp8(int fmt, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
                       const char *what) {
   if (EPI == EPI_SWIGLU_BWD) {
-    if (fmt == B_FP8_ROWSCALE) return launch_nt<192, 256, 2, 4, 2, EPI, B_FP8_ROWSCALE>(p, seg, M, s, what);
-    return launch_nt<192, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
+    if (fmt == B_FP8_ROWSCALE) return launch_nt<128, 256, 2, 4, 2, EPI, B_FP8_ROWSCALE>(p, seg, M, s, what);
+    return launch_nt<128, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
   }
   if (fmt == B_FP8_ROWSCALE) return launch_nt<256, 256, 2, 4, 2, EPI, B_FP8_ROWSCALE>(p, seg, M, s, what);
   return launch_nt<256, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);

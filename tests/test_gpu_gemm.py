@@ -286,7 +286,7 @@ def test_transpose(device):
     assert torch.equal(got.cpu(), (src.float() * 2).transpose(1, 2).to(torch.bfloat16))
 
 
-@pytest.mark.parametrize("tile", range(10))
+@pytest.mark.parametrize("tile", range(13))
 def test_every_tile_config(device, tile, monkeypatch):
     """All macro-tile configurations of the large kernels give the same products."""
     ops = _ops()
