@@ -84,6 +84,18 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Wait until at most `pend` (0 <= pend <= P) groups of G global loads are
+// outstanding: the oldest stage has landed.  pend is wave-uniform.
+template <int G, int P>
+__device__ __forceinline__ void wait_stages(int pend) {
+  if constexpr (P <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (pend >= P) wait_vmcnt<G * P>();
+    else wait_stages<G, P - 1>(pend);
+  }
+}
+
 // Workgroup barrier that waits for this wave's LDS reads/writes (lgkmcnt) but
 // not for its global loads: in-flight LDS-DMA prefetches of later stages stay
 // outstanding (a fenced __syncthreads would drain them with vmcnt(0)).
@@ -101,6 +113,18 @@ __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
 // MFMA operand reads (32 lanes on 32 consecutive rows) are conflict-free for
 // both a 32-bank (8 lanes x 16 B per cycle) and a 64-bank (16 lanes) LDS.
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// The same for 64-byte rows (32 bf16, the BK = 32 stages): 4 chunks per row,
+// chunk c of row r at physical chunk c ^ swz64(r).  A 128-byte bank window
+// holds two rows, so rows of equal parity among 8 consecutive rows (32-bank
+// LDS) and rows of equal r % 4 among 16 (64-bank LDS) must get distinct values.
+__device__ __forceinline__ int swz64(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+template <int BK>
+__device__ __forceinline__ int chunk_swz(int r) {
+  static_assert(BK == 32 || BK == 64, "k-tile of 32 or 64");
+  return BK == 64 ? swz(r) : swz64(r);
+}
 
 // One stage of operand DMA for this wave: A_PW blocks of A rows, B_PW of B rows.
 template <int A_PW, int B_PW, int A_BYTES>
@@ -131,41 +155,44 @@ __device__ __forceinline__ int b_source_row(int r, int nt, int N, int F) {
 }
 
 // Stage DMA for a partial k-tile: a chunk past klim re-reads the row's last
-// chunk (those columns are never multiplied).  The logical chunk of block b's
-// slot is (lane & 7) ^ swz(8b + lane / 8).
-template <int A_PW, int B_PW, int A_BYTES>
+// chunk (those columns are never multiplied).  A 1 KB block holds RPB rows of
+// CPR chunks; the logical chunk of block b's slot is
+// (lane % CPR) ^ chunk_swz(RPB b + lane / CPR).
+template <int A_PW, int B_PW, int A_BYTES, int BK = 64>
 __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, const char *abase,
                                                  const char *bbase, const uint32_t (&aoff)[A_PW],
                                                  const uint32_t (&boff)[B_PW], int kb, int klim) {
+  constexpr int CPR = BK / 8, RPB = 64 / CPR;
 #pragma unroll
   for (int i = 0; i < A_PW; ++i) {
     const int bi = wave * A_PW + i;
-    const int ch = (lane & 7) ^ swz(bi * 8 + (lane >> 3));
+    const int ch = (lane % CPR) ^ chunk_swz<BK>(bi * RPB + lane / CPR);
     const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
     dma16((const bf16 *)(abase + (aoff[i] + (uint32_t)(off * 2))), st + bi * 1024);
   }
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
     const int bi = wave * B_PW + i;
-    const int ch = (lane & 7) ^ swz(bi * 8 + (lane >> 3));
+    const int ch = (lane % CPR) ^ chunk_swz<BK>(bi * RPB + lane / CPR);
     const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
     dma16((const bf16 *)(bbase + (boff[i] + (uint32_t)(off * 2))), st + A_BYTES + bi * 1024);
   }
 }
 
-// MFMA operands of one 16-wide k step from a swizzled stage (rows of 64 bf16).
-template <int TM, int TN, int WTM, int WTN, int A_BYTES>
+// MFMA operands of one 16-wide k step from a swizzled stage (rows of BK bf16).
+template <int TM, int TN, int WTM, int WTN, int A_BYTES, int BK = 64>
 __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int wn, int lrow, int lk,
                                            bf16x8 (&af)[TM], bf16x8 (&bfv)[TN]) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int r = wm * WTM + i * 32 + lrow;
-    af[i] = *(const bf16x8 *)(st + r * 128 + (((kk * 2 + lk) ^ swz(r)) << 4));
+    af[i] = *(const bf16x8 *)(st + r * (2 * BK) + (((kk * 2 + lk) ^ chunk_swz<BK>(r)) << 4));
   }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int r = wn * WTN + j * 32 + lrow;
-    bfv[j] = *(const bf16x8 *)(st + A_BYTES + r * 128 + (((kk * 2 + lk) ^ swz(r)) << 4));
+    bfv[j] = *(const bf16x8 *)(st + A_BYTES + r * (2 * BK) +
+                               (((kk * 2 + lk) ^ chunk_swz<BK>(r)) << 4));
   }
 }
 
@@ -253,33 +280,36 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&a
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfv[j], af[i], acc[i][j], 0, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
-  constexpr int BK = 64;
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int CPR = BK / 8, RPB = 64 / CPR;  // 16-byte chunks per row, rows per 1 KB block
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int KSC_BYTES = BQ8 == B_FP8_KSCALE ? BK * 4 : 0;  // per-k scales of an fp8 k-tile
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES + KSC_BYTES;
-  constexpr int A_PW = BM / 8 / NW, B_PW = BN / 8 / NW;  // 1 KB DMA blocks per wave
-  constexpr int B_PW8 = BQ8 ? BN / 16 / NW : 1;           // fp8 B: 16 rows per 1 KB block
+  constexpr int A_PW = BM / RPB / NW, B_PW = BN / RPB / NW;  // 1 KB DMA blocks per wave
+  constexpr int B_PW8 = BQ8 ? BN / 16 / NW : 1;               // fp8 B: 16 rows per 1 KB block
   // DMA instructions per stage per wave.  With fp8 weights the base stages
   // issue fewer than the LoRA stages; waiting with the smaller count is
   // conservative for both (the per-k scale DMA of wave 0 likewise).
   constexpr int G = BQ8 ? A_PW + B_PW8 : A_PW + B_PW;
   constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+  constexpr int RED_BYTES = EPI == EPI_SWIGLU_BWD ? WN * BM * 4 : 0;  // dp row partials
   constexpr int UMASK = (BN / 4 >= 32) ? 31 : (BN / 4 - 1);  // staging swizzle (8-byte units)
   static_assert(TM >= 1 && TN >= 1 && A_PW >= 1 && B_PW >= 1, "tile config");
-  static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "DMA blocks must split across waves");
+  static_assert((BM / RPB) % NW == 0 && (BN / RPB) % NW == 0, "DMA blocks must split across waves");
+  static_assert(BK == 64 || BQ8 == B_BF16, "fp8 weights use 64-wide k-tiles");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN % 2 == 0), "SwiGLU forward pairs gate/up blocks");
   static_assert(BM * BN * 2 <= LDS_BYTES, "epilogue staging must fit the LDS ring");
-  static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 4, "vmcnt range");
+  static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 6, "vmcnt range");
+  static_assert(LDS_BYTES + RED_BYTES <= 160 * 1024, "LDS of one workgroup");
   static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
   static_assert(!BQ8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
 
-  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
-  __shared__ float sRed[EPI == EPI_SWIGLU_BWD ? WN * BM : 1];
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES];
+  float *sRed = (float *)(smem + LDS_BYTES);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -291,9 +321,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   const int nk_main = (p.K + BK - 1) / BK;
   const int nk = nk_main + (p.kt + BK - 1) / BK;
   const int nk_full = p.K / BK;  // full 64-wide k-tiles of the base product
-  // DMA slot of this lane inside a 1 KB block (8 rows): row lane/8, physical
-  // chunk lane%8, holding logical chunk (lane%8) ^ swz(row).
-  const int drow = lane >> 3;
+  // DMA slot of this lane inside a 1 KB block (RPB rows): row lane/CPR,
+  // physical chunk lane%CPR, holding logical chunk (lane%CPR) ^ chunk_swz(row).
+  const int drow = lane / CPR, dch = lane % CPR;
 
   for (int tile = lb; tile < total; tile += nb) {
     const int mt = tile / n_tiles, nt = tile - mt * n_tiles;
@@ -315,10 +345,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     uint32_t aoff[A_PW], boff[BQ8 ? B_PW8 : B_PW];
 #pragma unroll
     for (int i = 0; i < A_PW; ++i) {
-      int m = m0 + (wave * A_PW + i) * 8 + drow;
+      int m = m0 + (wave * A_PW + i) * RPB + drow;
       m = m < m_end ? m : m_end - 1;
       const uint32_t src = p.a_rows ? (uint32_t)p.a_rows[m] : (uint32_t)m;
-      const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * A_PW + i) * 8 + drow));
+      const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>((wave * A_PW + i) * RPB + drow));
       aoff[i] = (src * (uint32_t)p.lda + ch * 8) * 2u;
     }
     if (BQ8) {
@@ -332,9 +362,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     } else {
 #pragma unroll
       for (int i = 0; i < B_PW; ++i) {
-        const int r = (wave * B_PW + i) * 8 + drow;
+        const int r = (wave * B_PW + i) * RPB + drow;
         const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
-        const uint32_t ch = (uint32_t)((lane & 7) ^ swz(r));
+        const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>(r));
         boff[i] = ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
       }
     }
@@ -354,21 +384,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   do {                                                                                        \
     uint32_t toff_[A_PW], loff_[B_PW];                                                        \
     _Pragma("unroll") for (int i = 0; i < A_PW; ++i) {                                        \
-      int m = m0 + (wave * A_PW + i) * 8 + drow;                                              \
+      int m = m0 + (wave * A_PW + i) * RPB + drow;                                            \
       m = m < m_end ? m : m_end - 1;                                                          \
-      const uint32_t ch = (uint32_t)((lane & 7) ^ swz((wave * A_PW + i) * 8 + drow));         \
+      const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>((wave * A_PW + i) * RPB + drow));    \
       toff_[i] = ((uint32_t)m * (uint32_t)p.ldt + ch * 8) * 2u;                               \
     }                                                                                         \
     _Pragma("unroll") for (int i = 0; i < B_PW; ++i) {                                        \
-      const int r = (wave * B_PW + i) * 8 + drow;                                             \
+      const int r = (wave * B_PW + i) * RPB + drow;                                           \
       const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);                                   \
-      const uint32_t ch = (uint32_t)((lane & 7) ^ swz(r));                                    \
+      const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>(r));                                 \
       loff_[i] = ((uint32_t)n * (uint32_t)p.ldl + ch * 8) * 2u;                               \
     }                                                                                         \
-    issue_stage_tail<A_PW, B_PW, A_BYTES>(smem + ((ks) % STAGES) * STAGE_BYTES, wave, lane,  \
-                                          (const char *)p.t,                                  \
-                                          (const char *)(p.l + (int64_t)e * p.l_es), toff_,   \
-                                          loff_, ((ks) - nk_main) * BK, p.kt);                \
+    issue_stage_tail<A_PW, B_PW, A_BYTES, BK>(                                                \
+        smem + ((ks) % STAGES) * STAGE_BYTES, wave, lane, (const char *)p.t,                  \
+        (const char *)(p.l + (int64_t)e * p.l_es), toff_, loff_, ((ks) - nk_main) * BK, p.kt); \
   } while (0)
 
 #define ART_ISSUE(ks)                                                                         \
@@ -387,8 +416,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       }                                                                                       \
     } else if ((ks) < nk_main) {                                                              \
       if constexpr (BQ8 == B_BF16)                                                            \
-        issue_stage_tail<A_PW, B_PW, A_BYTES>(st_, wave, lane, abase, bbase, aoff, boff,      \
-                                              (ks) * BK, p.K);                                \
+        issue_stage_tail<A_PW, B_PW, A_BYTES, BK>(st_, wave, lane, abase, bbase, aoff, boff,  \
+                                                  (ks) * BK, p.K);                            \
     } else {                                                                                  \
       ART_ISSUE_LORA(ks);                                                                     \
     }                                                                                         \
@@ -412,16 +441,38 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #define ART_STAGE_IN(ks)                                                                      \
   do {                                                                                        \
     const int pend_ = (nk - 1 - (ks)) < (STAGES - 2) ? (nk - 1 - (ks)) : (STAGES - 2);        \
-    if (STAGES == 2 || pend_ == 0) wait_vmcnt<0>();                                           \
-    else if (STAGES == 3 || pend_ == 1) wait_vmcnt<(STAGES >= 3 ? G : 0)>();                  \
-    else wait_vmcnt<(STAGES >= 4 ? 2 * G : 0)>();                                             \
+    wait_stages<G, STAGES - 2>(pend_);                                                        \
     barrier_nofence();                                                                        \
     if ((ks) + STAGES - 1 < nk) ART_ISSUE((ks) + STAGES - 1);                                 \
   } while (0)
 
-    // Full 64-wide k-tiles of the base product: branch-free, fragments of step
-    // kk+1 are read while step kk multiplies.  (A separate loop keeps the
+    // Full k-tiles of the base product: branch-free, fragments of step kk+1
+    // are read while step kk multiplies.  (A separate loop keeps the
     // accumulators in one register assignment across iterations.)
+    if constexpr (BK == 32) {
+      // Two k-steps per stage.  The wait + barrier for stage ks+1 sits between
+      // the two steps of stage ks: after it, every wave has finished reading
+      // stage ks (its slot takes stage ks+STAGES) and stage ks+1 is visible, so
+      // its first fragments load while the second step of ks multiplies.
+      bf16x8 af0[TM], bf0[TN], af1[TM], bf1[TN];
+      if (nk_full > 0) {
+        ART_STAGE_IN(0);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem, 0, wm, wn, lrow, lk, af0, bf0);
+      }
+      for (int ks = 0; ks < nk_full; ++ks) {
+        const char *st = smem + (ks % STAGES) * STAGE_BYTES;
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, 1, wm, wn, lrow, lk, af1, bf1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_step<TM, TN>(acc, af0, bf0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < nk) ART_STAGE_IN(ks + 1);
+        if (ks + 1 < nk_full)
+          load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem + ((ks + 1) % STAGES) * STAGE_BYTES, 0,
+                                                    wm, wn, lrow, lk, af0, bf0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_step<TM, TN>(acc, af1, bf1);
+      }
+    } else {
     for (int ks = 0; ks < nk_full; ++ks) {
       ART_STAGE_IN(ks);
       const char *st = smem + (ks % STAGES) * STAGE_BYTES;
@@ -461,9 +512,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       mma_step<TM, TN>(acc, af1, bf1);
 #undef ART_FENCE
     }
-    // Tail: a partial base k-tile and the LoRA K-extension tiles.
+    }
+    // Tail: a partial base k-tile and the LoRA K-extension tiles.  (With
+    // BK = 32 the last full k-tile already brought stage nk_full in.)
     for (int ks = nk_full; ks < nk; ++ks) {
-      ART_STAGE_IN(ks);
+      if (BK == 64 || nk_full == 0 || ks > nk_full) ART_STAGE_IN(ks);
       const char *st = smem + (ks % STAGES) * STAGE_BYTES;
       const bool main = ks < nk_main;
       const int kb = (main ? ks : ks - nk_main) * BK;
@@ -471,7 +524,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       const int nkk = (klim - kb) >= BK ? BK / 16 : (klim - kb) / 16;
       for (int kk = 0; kk < nkk; ++kk) {
         bf16x8 af[TM], bfv[TN];
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, kk, wm, wn, lrow, lk, af, bfv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, kk, wm, wn, lrow, lk, af, bfv);
         mma_step<TM, TN>(acc, af, bfv);
       }
     }
@@ -678,7 +731,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
                      const char *what) {
   constexpr int bmi = BM / 64 - 1;  // segment-table row of this tile height
@@ -689,7 +742,8 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   if (occ == 0) {
     int o = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8>, NT, 0) != hipSuccess || o < 1)
+            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8, BK>, NT, 0) != hipSuccess ||
+        o < 1)
       o = 1;
     occ = o;
   }
@@ -702,7 +756,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   if (grid > max_tiles) grid = max_tiles;
   if (grid >= 8) grid &= ~(int64_t)7;
   if (grid < 1) grid = 1;
-  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8><<<dim3((unsigned)grid), NT, 0, s>>>(p);
+  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8, BK><<<dim3((unsigned)grid), NT, 0, s>>>(p);
   return check_launch(what);
 }
 
@@ -713,7 +767,10 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
 // 6: 256x256 (4x2, 2)               7: 256x256 (2x2, 2: 128x128 per wave)
 // 8: 192x256 (2x4, 2)               9: 192x128 (2x2, 3)  10: 128x128 (2x2, 2)
 // 11: 128x256 (2x4, 2)             12: 256x128 (4x2, 2)
-enum { kNumTileCfgs = 13 };
+// with 32-wide k-tiles (half-size stages, deeper rings):
+// 13: 256x256 (2x4, 4)  14: 256x256 (2x4, 5; 4 for the SwiGLU backward)
+// 15: 128x256 (2x4, 4)  16: 128x256 (2x4, 6)  17: 256x128 (4x2, 6)
+enum { kNumTileCfgs = 18 };
 // Defaults from a sweep of the C1 products on MI355X.
 enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 11 };
 
@@ -733,6 +790,15 @@ static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, h
     case 10: return launch_nt<128, 128, 2, 2, 2, EPI>(p, seg, M, s, what);
     case 11: return launch_nt<128, 256, 2, 4, 2, EPI>(p, seg, M, s, what);
     case 12: return launch_nt<256, 128, 4, 2, 2, EPI>(p, seg, M, s, what);
+    case 13: return launch_nt<256, 256, 2, 4, 4, EPI, B_BF16, 32>(p, seg, M, s, what);
+    case 14:
+      if constexpr (EPI == EPI_SWIGLU_BWD)  // the dp partials do not fit beside 5 stages
+        return launch_nt<256, 256, 2, 4, 4, EPI, B_BF16, 32>(p, seg, M, s, what);
+      else
+        return launch_nt<256, 256, 2, 4, 5, EPI, B_BF16, 32>(p, seg, M, s, what);
+    case 15: return launch_nt<128, 256, 2, 4, 4, EPI, B_BF16, 32>(p, seg, M, s, what);
+    case 16: return launch_nt<128, 256, 2, 4, 6, EPI, B_BF16, 32>(p, seg, M, s, what);
+    case 17: return launch_nt<256, 128, 4, 2, 6, EPI, B_BF16, 32>(p, seg, M, s, what);
     default: return launch_nt<256, 256, 2, 2, 2, EPI>(p, seg, M, s, what);
   }
 }

@@ -286,7 +286,10 @@ def test_transpose(device):
     assert torch.equal(got.cpu(), (src.float() * 2).transpose(1, 2).to(torch.bfloat16))
 
 
-@pytest.mark.parametrize("tile", range(13))
+N_TILE_CFGS = 18  # kNumTileCfgs of gemm.hip
+
+
+@pytest.mark.parametrize("tile", range(N_TILE_CFGS))
 def test_every_tile_config(device, tile, monkeypatch):
     """All macro-tile configurations of the large kernels give the same products."""
     ops = _ops()
@@ -321,3 +324,31 @@ def test_every_tile_config(device, tile, monkeypatch):
     (torch.nn.functional.silu(a_) * b_ * p[:, None]).backward(dh)
     assert rel(dy1, y1f.grad) < 1e-2
     assert rel(dp_part.sum(0), p.grad) < 1e-3
+
+
+@pytest.mark.parametrize("tile", range(N_TILE_CFGS))
+@pytest.mark.parametrize("k", [16, 528])
+def test_tile_config_partial_k(device, tile, k, monkeypatch):
+    """Ragged K: no full k-tile (K=16) or a partial last one (K=528), and a
+    LoRA extension (kt=48) that spans a full and a partial k-tile of the
+    32-wide configurations."""
+    ops = _ops()
+    monkeypatch.setenv("ART_MOE_GEMM_TILE", str(tile))
+    print(f"tile config {tile} K={k}", flush=True)
+    g = torch.Generator().manual_seed(7 * tile + k)
+    e, m, f, kt = 5, 700, 192, 48
+    counts = _counts(e, m, seed=tile + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(e, 2 * f, k, generator=g) * 0.1).to(torch.bfloat16)
+    tl = torch.randn(m, kt, generator=g).to(torch.bfloat16)
+    l1 = (torch.randn(e, 2 * f, kt, generator=g) * 0.05).to(torch.bfloat16)
+    prob = torch.rand(m, generator=g)
+    seg = ops.segments_from_counts(counts, e, device)
+    ref = _ref_grouped(x.float(), w1, counts, tl, l1)
+    c = ops.grouped_gemm(x.to(device), w1.to(device), seg, e, m=m, tl=tl.to(device), l=l1.to(device))
+    assert rel(c, ref) < 1e-2
+    y1, hh = ops.fc1_swiglu(x.to(device), w1.to(device), seg, e, prob.to(device), m=m,
+                            tl=tl.to(device), l1=l1.to(device))
+    assert rel(y1, ref) < 1e-2
+    gg, uu = y1.cpu().float().chunk(2, dim=1)
+    assert rel(hh, torch.nn.functional.silu(gg) * uu * prob[:, None]) < 1e-2
