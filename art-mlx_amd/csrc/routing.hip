@@ -303,30 +303,54 @@ __global__ __launch_bounds__(256) void combine_kernel(
   const float my_dl = (act && w_r) ? dl[t * k + lane] : 0.0f;
   // The chunk loop is uniform across the wavefront (every lane runs every
   // iteration) so that the slot broadcasts below always read active lanes.
+  // Slots go in blocks of 8 whose row loads are all issued before the first
+  // is accumulated (8 loads in flight per lane instead of a chain of k); the
+  // accumulation order stays slot-ascending.  Slot j >= k reads lane j's
+  // inactive dest (-1).
   for (int c0 = 0; c0 < H8; c0 += kWave) {
     const int c = c0 + lane;
     const bool on = c < H8;
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      const int d = __shfl(my_dest, j, kWave);
-      const float wj = __shfl(my_w, j, kWave);
-      if (d < 0 || !on) continue;
-      float f[8];
-      unpack8(yp[(int64_t)d * H8 + c], f);
+    for (int jb = 0; jb < k; jb += 8) {
+      U4 v[8];
+      int dj[8];
+      float wj[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += wj * f[i];
+      for (int u = 0; u < 8; ++u) {
+        dj[u] = __shfl(my_dest, jb + u, kWave);
+        wj[u] = __shfl(my_w, jb + u, kWave);
+        v[u] = (dj[u] >= 0 && on) ? yp[(int64_t)dj[u] * H8 + c] : U4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (dj[u] < 0) continue;
+        float f[8];
+        unpack8(v[u], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += wj[u] * f[i];
+      }
     }
     if (w_r) {
-      for (int j = 0; j < k; ++j) {
-        const int e = __shfl(my_e, j, kWave);
-        const float lj = __shfl(my_dl, j, kWave);
-        if (e < 0 || !on) continue;
-        float f[8];
-        unpack8(w_r[(int64_t)e * H8 + c], f);
+      for (int jb = 0; jb < k; jb += 8) {
+        U4 v[8];
+        int ej[8];
+        float lj[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += lj * f[i];
+        for (int u = 0; u < 8; ++u) {
+          ej[u] = __shfl(my_e, jb + u, kWave);
+          lj[u] = __shfl(my_dl, jb + u, kWave);
+          v[u] = (ej[u] >= 0 && on) ? w_r[(int64_t)ej[u] * H8 + c] : U4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (ej[u] < 0) continue;
+          float f[8];
+          unpack8(v[u], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] += lj[u] * f[i];
+        }
       }
     }
     if (addend && on) {

@@ -140,7 +140,8 @@ def test_segments_from_counts(device):
     assert seg.cpu().numpy().tolist() == _seg_expect(counts, len(counts)).tolist()
 
 
-@pytest.mark.parametrize("t,h,e,k", [(8192, 2048, 128, 8), (33, 256, 8, 2), (5, 8, 4, 3)])
+@pytest.mark.parametrize("t,h,e,k", [(8192, 2048, 128, 8), (33, 256, 8, 2), (5, 8, 4, 3),
+                                     (300, 512, 64, 12), (100, 64, 40, 32)])
 def test_permute_and_combine_bit_exact(device, t, h, e, k):
     ops = _ops()
     print(f"permute/combine t={t} h={h}", flush=True)
@@ -167,3 +168,31 @@ def test_permute_and_combine_bit_exact(device, t, h, e, k):
     for j in range(k):
         acc = acc + wgt[:, j:j + 1].double() * yp[dest[:, j]].double()
     torch.testing.assert_close(y.cpu().double(), acc, rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("k", [8, 12, 20])
+def test_combine_router_grad_addend_and_dropped_slots(device, k):
+    """Backward combine: sum_j wgt y_perm[dest] + sum_j dl w_r[idx] + addend, with
+    some slots dropped (dest = -1), k spanning one to three blocks of 8 slots."""
+    ops = _ops()
+    print(f"combine backward k={k}", flush=True)
+    t, h, e = 200, 256, 48
+    g = torch.Generator().manual_seed(k)
+    m = t * k
+    dest = torch.randperm(m, generator=g).view(t, k).to(torch.int32)
+    dest[torch.rand(t, k, generator=g) < 0.1] = -1
+    yp = torch.randn(m, h, generator=g).to(torch.bfloat16)
+    wgt = torch.rand(t, k, generator=g)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)]).to(torch.int32)
+    dl = torch.randn(t, k, generator=g)
+    w_r = (torch.randn(e, h, generator=g) * 0.1).to(torch.bfloat16)
+    addend = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    y = ops.combine(yp.to(device), dest.to(device), t, wgt=wgt.to(device), dl=dl.to(device),
+                    idx=idx.to(device), w_r=w_r.to(device), addend=addend.to(device))
+    ref = addend.double().clone()
+    for j in range(k):
+        d = dest[:, j].long()
+        ok = (d >= 0).double().unsqueeze(1)
+        ref += ok * wgt[:, j:j + 1].double() * yp[d.clamp_min(0)].double()
+        ref += dl[:, j:j + 1].double() * w_r[idx[:, j].long()].double()
+    torch.testing.assert_close(y.cpu().double(), ref, rtol=2 ** -7, atol=1e-5)
