@@ -29,6 +29,7 @@ WGRAD_STORE_BF16 = 2
 B_BF16 = 0
 B_FP8_ROWSCALE = 1
 B_FP8_KSCALE = 2
+AB_FP8 = 3
 
 
 def seg_len(num_experts: int) -> int:
@@ -53,13 +54,13 @@ SIGNATURES = {
     "art_moe_segments_from_counts": (_I32, [_P, _I32, _P, _P]),
     "art_moe_permute": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P]),
     "art_moe_combine": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _P]),
-    "art_moe_grouped_gemm": (_I32, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _I32, _P, _I64, _P,
+    "art_moe_grouped_gemm": (_I32, [_P, _I64, _P, _P, _P, _I64, _I64, _P, _I64, _I32, _P, _I64, _P,
                                     _I64, _I64, _I32, _P, _I32, _I64, _I32, _I32, _F, _P, _I64,
                                     _I32, _P]),
-    "art_moe_fc1_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I32, _P, _I64, _P, _I32, _P, _I32, _I64,
+    "art_moe_fc1_swiglu": (_I32, [_P, _I64, _P, _P, _P, _P, _I32, _P, _I64, _P, _I32, _P, _I32, _I64,
                                   _I32, _I32, _P, _P, _P, _P]),
     "art_moe_dgrad_swiglu_parts": (_I32, [_I32]),
-    "art_moe_fc2_dgrad_swiglu": (_I32, [_P, _I64, _P, _P, _P, _I32, _P, _I64, _P, _I32, _P, _I32,
+    "art_moe_fc2_dgrad_swiglu": (_I32, [_P, _I64, _P, _P, _P, _P, _I32, _P, _I64, _P, _I32, _P, _I32,
                                         _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32, _F,
                                      _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P,
@@ -71,6 +72,8 @@ SIGNATURES = {
     "art_moe_weighted_swiglu_back": (_I32, [_P, _P, _P, _I64, _I32, _P, _P, _P]),
     "art_moe_router_lora_apply": (_I32, [_P, _I64, _I32, _P, _I32, _F, _P, _P, _P]),
     "art_moe_router_lora_grad": (_I32, [_P, _P, _I64, _I32, _P, _I32, _I32, _F, _P, _P, _P]),
+    "art_moe_quantize_rows_fp8": (_I32, [_P, _I64, _P, _P, _I32, _P, _I64, _I64, _I32, _P, _I64,
+                                         _P, _P]),
 }
 
 

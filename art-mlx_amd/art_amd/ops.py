@@ -167,9 +167,21 @@ def combine(y_perm: torch.Tensor, dest: torch.Tensor, num_tokens: int, *,
 FP8_DTYPES = (torch.float8_e4m3fn, torch.uint8)
 
 
-def _weight_format(b: torch.Tensor, b_scale: torch.Tensor | None, per_k: bool):
+def _weight_format(b: torch.Tensor, b_scale: torch.Tensor | None, per_k: bool,
+                   a_scale: torch.Tensor | None = None):
     """(format code, scale pointer, scale expert stride) of a weight operand:
-    bf16, or fp8 e4m3fn bytes (float8_e4m3fn or uint8 view) with fp32 scales."""
+    bf16, or fp8 e4m3fn bytes (float8_e4m3fn or uint8 view) with fp32 scales.
+    With ``a_scale`` (fp8 activations too, W8A8) the weight is fp8 and
+    ``b_scale`` an optional per-row [E, N] scale."""
+    if a_scale is not None:
+        _need(b.dtype in FP8_DTYPES, "fp8 activations need fp8 weights")
+        _need(a_scale.dtype == torch.float32 and a_scale.dim() == 1 and a_scale.is_contiguous(),
+              "a_scale must be contiguous fp32 [rows]")
+        if b_scale is None:
+            return _lib.AB_FP8, None, 0
+        _need(b_scale.dtype == torch.float32 and b_scale.is_contiguous() and b_scale.dim() == 2
+              and b_scale.shape == b.shape[:2], "W8A8 weight scales must be fp32 [E, N]")
+        return _lib.AB_FP8, b_scale, b_scale.stride(0)
     if b.dtype == torch.bfloat16:
         _need(b_scale is None, "bf16 weights take no scale")
         return _lib.B_BF16, None, 0
@@ -185,16 +197,19 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
                  tl: torch.Tensor | None = None, l: torch.Tensor | None = None,
                  alpha: float = 1.0, out_fp32: bool = False,
                  out: torch.Tensor | None = None, b_scale: torch.Tensor | None = None,
-                 scale_per_k: bool = False) -> torch.Tensor:
+                 scale_per_k: bool = False, a_scale: torch.Tensor | None = None) -> torch.Tensor:
     """C = alpha * (A[row(m)] @ B[e]^T + Tl @ L[e]^T) per expert segment.
 
     a [*, K] bf16; b [E, N, K] bf16 (last dim contiguous), or fp8 e4m3fn with
     ``b_scale`` [E, N] (per row) / [E, K] (``scale_per_k``): B = bf16(q * s);
-    tl [M, kt], l [E, N, kt].
+    tl [M, kt], l [E, N, kt].  W8A8: ``a`` fp8 e4m3fn with ``a_scale`` per A
+    source row (``quantize_rows_fp8``), fp8 ``b`` with optional per-row
+    ``b_scale``; the fp8 MFMA computes s_a s_b (A_q B_q^T).
     """
-    _cuda(a, b, seg, a_rows, tl, l, b_scale)
-    _need(a.dtype == torch.bfloat16, "A must be bf16")
-    fmt, bsc, bs_es = _weight_format(b, b_scale, scale_per_k)
+    _cuda(a, b, seg, a_rows, tl, l, b_scale, a_scale)
+    _need(a.dtype == torch.bfloat16 or (a_scale is not None and a.dtype in FP8_DTYPES),
+          "A must be bf16 (or fp8 with a_scale)")
+    fmt, bsc, bs_es = _weight_format(b, b_scale, scale_per_k, a_scale)
     _need(b.dim() == 3 and b.shape[0] == num_experts, "B must be [E, N, K]")
     n, k = b.shape[1], b.shape[2]
     _need(a.shape[-1] == k, f"A has K={a.shape[-1]}, B has K={k}")
@@ -209,7 +224,8 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
         ldt, ldl, l_es = _rowmajor(tl, "Tl"), _rowmajor(l, "L"), l.stride(0)
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32 if out_fp32 else torch.bfloat16, device=a.device)
-    call("art_moe_grouped_gemm", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(b), _rowmajor(b, "B"),
+    call("art_moe_grouped_gemm", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(a_scale), ptr(b),
+         _rowmajor(b, "B"),
          b.stride(0), ptr(bsc), bs_es, fmt, ptr(tl), ldt, ptr(l), ldl, l_es, kt, ptr(seg),
          num_experts, m, n, k,
          float(alpha), ptr(out), _rowmajor(out, "C"), int(out.dtype == torch.float32),
@@ -220,14 +236,15 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
 def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts: int,
                row_prob: torch.Tensor, *, m: int, a_rows: torch.Tensor | None = None,
                tl: torch.Tensor | None = None, l1: torch.Tensor | None = None,
-               w1_scale: torch.Tensor | None = None):
+               w1_scale: torch.Tensor | None = None, a_scale: torch.Tensor | None = None):
     """(y1 [M,2F], h [M,F]) = FC1 (+LoRA) then weighted SwiGLU, fused.
-    ``w1`` is bf16, or fp8 e4m3fn with per-row scales ``w1_scale`` [E, 2F]."""
-    _cuda(a, w1, seg, row_prob, a_rows, tl, l1, w1_scale)
+    ``w1`` is bf16, or fp8 e4m3fn with per-row scales ``w1_scale`` [E, 2F];
+    with ``a_scale`` the activations are fp8 too (W8A8, see grouped_gemm)."""
+    _cuda(a, w1, seg, row_prob, a_rows, tl, l1, w1_scale, a_scale)
     e, f2, k = w1.shape
     f = f2 // 2
     _need(w1.is_contiguous(), "w1 must be contiguous [E, 2F, K]")
-    fmt, wsc, _ = _weight_format(w1, w1_scale, False)
+    fmt, wsc, _ = _weight_format(w1, w1_scale, False, a_scale)
     kt = 0
     ldt = 0
     if tl is not None:
@@ -236,7 +253,8 @@ def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts
         ldt = _rowmajor(tl, "Tl")
     y1 = torch.empty((m, f2), dtype=torch.bfloat16, device=a.device)
     h = torch.empty((m, f), dtype=torch.bfloat16, device=a.device)
-    call("art_moe_fc1_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w1), ptr(wsc), fmt,
+    call("art_moe_fc1_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(a_scale), ptr(w1),
+         ptr(wsc), fmt,
          ptr(tl), ldt,
          ptr(l1), kt, ptr(seg), num_experts, m, f, k, ptr(row_prob), ptr(y1), ptr(h),
          stream_ptr(a.device))
@@ -250,13 +268,16 @@ def dgrad_swiglu_parts(f: int) -> int:
 def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_experts: int,
                      y1: torch.Tensor, row_prob: torch.Tensor, *, m: int,
                      a_rows: torch.Tensor | None = None, tl: torch.Tensor | None = None,
-                     l2: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None):
+                     l2: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
+                     a_scale: torch.Tensor | None = None):
     """(dy1 [M,2F] bf16, dp_part [n_parts, M] fp32) of the FC2 dgrad + SwiGLU backward.
-    ``w2t`` is bf16, or fp8 e4m3fn with the FC2 row scales ``w2_scale`` [E, K]."""
-    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2, w2_scale)
+    ``w2t`` is bf16, or fp8 e4m3fn with the FC2 row scales ``w2_scale`` [E, K].
+    W8A8 (``a_scale``): ``a`` is fp8 with the FC2 row scales already folded in
+    (``quantize_rows_fp8(..., col_scale=w2_scale)``) and ``w2_scale`` is None."""
+    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2, w2_scale, a_scale)
     e, f, k = w2t.shape
     _need(w2t.is_contiguous(), "w2t must be contiguous [E, F, K]")
-    fmt, wsc, _ = _weight_format(w2t, w2_scale, True)
+    fmt, wsc, _ = _weight_format(w2t, w2_scale, True, a_scale)
     _need(y1.is_contiguous() and y1.shape == (m, 2 * f), "y1 must be contiguous [M, 2F]")
     kt = 0
     ldt = 0
@@ -266,11 +287,37 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
         ldt = _rowmajor(tl, "Tl")
     dy1 = torch.empty((m, 2 * f), dtype=torch.bfloat16, device=a.device)
     dp_part = torch.empty((dgrad_swiglu_parts(f), m), dtype=torch.float32, device=a.device)
-    call("art_moe_fc2_dgrad_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(w2t), ptr(wsc),
+    call("art_moe_fc2_dgrad_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(a_scale), ptr(w2t),
+         ptr(wsc),
          fmt, ptr(tl), ldt,
          ptr(l2), kt, ptr(seg), num_experts, m, f, k, ptr(y1), ptr(row_prob), ptr(dy1),
          ptr(dp_part), stream_ptr(a.device))
     return dy1, dp_part
+
+
+def quantize_rows_fp8(src: torch.Tensor, *, rows: torch.Tensor | None = None,
+                      seg: torch.Tensor | None = None, num_experts: int = 0,
+                      col_scale: torch.Tensor | None = None, m: int | None = None):
+    """(q [M, K] float8_e4m3fn, row_scale [M] fp32): per-row e4m3fn quantisation
+    of bf16 rows ``src[rows[m]]`` (or ``src[m]``), optionally times the
+    per-expert column scales ``col_scale`` [E, K] of row m's expert segment in
+    ``seg``.  row_scale = amax / 448 (1 for a zero row)."""
+    _cuda(src, rows, seg, col_scale)
+    _need(src.dtype == torch.bfloat16 and src.dim() == 2, "src must be bf16 [rows, K]")
+    k = src.shape[1]
+    if m is None:
+        m = rows.shape[0] if rows is not None else src.shape[0]
+    cs_es = 0
+    if col_scale is not None:
+        _need(col_scale.dtype == torch.float32 and col_scale.is_contiguous() and col_scale.dim() == 2
+              and col_scale.shape[1] == k and seg is not None, "col_scale must be fp32 [E, K] with seg")
+        cs_es = col_scale.stride(0)
+        num_experts = col_scale.shape[0]
+    q = torch.empty((m, k), dtype=torch.float8_e4m3fn, device=src.device)
+    sc = torch.empty((m,), dtype=torch.float32, device=src.device)
+    call("art_moe_quantize_rows_fp8", ptr(src), _rowmajor(src, "src"), ptr(rows), ptr(seg),
+         int(num_experts), ptr(col_scale), cs_es, m, k, ptr(q), k, ptr(sc), stream_ptr(src.device))
+    return q, sc
 
 
 def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_experts: int, *,

@@ -42,6 +42,7 @@ struct NTArgs {
   const bf16 *a;
   int64_t lda;
   const int32_t *a_rows;
+  const float *a_scale;  // fp8 A (AB_FP8): scale per A source row
   const bf16 *b;      // bf16 [E][N][ldb], or fp8 e4m3fn bytes with b_scale
   int64_t ldb;
   int64_t b_es;
@@ -200,7 +201,7 @@ __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int w
 // moved in 1 KB DMA blocks of 16 rows; 16-byte chunk c of row r lives at
 // physical chunk c ^ swz8(r).
 enum { B_BF16 = ART_MOE_B_BF16, B_FP8_ROWSCALE = ART_MOE_B_FP8_ROWSCALE,
-       B_FP8_KSCALE = ART_MOE_B_FP8_KSCALE };
+       B_FP8_KSCALE = ART_MOE_B_FP8_KSCALE, B_FP8_AB = ART_MOE_AB_FP8 };
 
 __device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
@@ -268,6 +269,54 @@ __device__ __forceinline__ void load_frags8(const char *st, int kk, int wm, int 
   }
 }
 
+// fp8 A x fp8 B (AB_FP8): 64-byte LDS rows hold 64 e4m3fn values of one
+// k-tile (chunk c of row r at physical chunk c ^ swz64(r)); one
+// v_mfma_scale_f32_32x32x64_f8f6f4 step per 32x32 block covers the k-tile.
+// Lane l takes row l%32 and the 32 bytes k = 32*(l/32) .. +31 of both
+// operands: the same lane -> k assignment for A and B, so every product pairs
+// equal k whatever order the instruction sums in.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+template <int TM, int TN, int WTM, int WTN, int A_BYTES>
+__device__ __forceinline__ void load_frags_f8(const char *st, int wm, int wn, int lrow, int lk,
+                                              i32x8 (&af)[TM], i32x8 (&bfv)[TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = wm * WTM + i * 32 + lrow;
+    const int4 lo = *(const int4 *)(st + r * 64 + (((2 * lk) ^ swz64(r)) << 4));
+    const int4 hi = *(const int4 *)(st + r * 64 + (((2 * lk + 1) ^ swz64(r)) << 4));
+    af[i] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int r = wn * WTN + j * 32 + lrow;
+    const int4 lo = *(const int4 *)(st + A_BYTES + r * 64 + (((2 * lk) ^ swz64(r)) << 4));
+    const int4 hi = *(const int4 *)(st + A_BYTES + r * 64 + (((2 * lk + 1) ^ swz64(r)) << 4));
+    bfv[j] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void mma_step_f8(f32x16 (&acc)[TM][TN], const i32x8 (&af)[TM],
+                                            const i32x8 (&bfv)[TN]) {
+  // formats 0/0 = fp8 e4m3 for both operands; e8m0 scales 127 = 1.0
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bfv[j], af[i], acc[i][j], 0, 0,
+                                                                  0, 127, 0, 127);
+}
+
+// bf16 fragment times a scale, rounded back to bf16 (LoRA operands of the
+// AB_FP8 products, divided by the row scales the epilogue multiplies back).
+__device__ __forceinline__ bf16x8 scale_frag(bf16x8 v, float s) {
+  bf16x8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = (bf16)((float)v[i] * s);
+  return o;
+}
+
 // B is the MFMA's first operand: acc[i][j] accumulates the transposed block,
 // so each lane ends up with 4 consecutive output columns of one row.
 template <int TM, int TN>
@@ -285,28 +334,32 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr bool W8 = BQ8 == B_FP8_ROWSCALE || BQ8 == B_FP8_KSCALE;  // fp8 B, bf16 A
+  constexpr bool A8 = BQ8 == B_FP8_AB;                               // fp8 A and B
+  constexpr int KPS = A8 ? 2 * BK : BK;  // base-product k per stage (64-byte rows: 64 fp8)
   constexpr int CPR = BK / 8, RPB = 64 / CPR;  // 16-byte chunks per row, rows per 1 KB block
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int KSC_BYTES = BQ8 == B_FP8_KSCALE ? BK * 4 : 0;  // per-k scales of an fp8 k-tile
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES + KSC_BYTES;
   constexpr int A_PW = BM / RPB / NW, B_PW = BN / RPB / NW;  // 1 KB DMA blocks per wave
-  constexpr int B_PW8 = BQ8 ? BN / 16 / NW : 1;               // fp8 B: 16 rows per 1 KB block
+  constexpr int B_PW8 = W8 ? BN / 16 / NW : 1;                // fp8 B: 16 rows per 1 KB block
   // DMA instructions per stage per wave.  With fp8 weights the base stages
   // issue fewer than the LoRA stages; waiting with the smaller count is
   // conservative for both (the per-k scale DMA of wave 0 likewise).
-  constexpr int G = BQ8 ? A_PW + B_PW8 : A_PW + B_PW;
+  constexpr int G = W8 ? A_PW + B_PW8 : A_PW + B_PW;
   constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
   constexpr int RED_BYTES = EPI == EPI_SWIGLU_BWD ? WN * BM * 4 : 0;  // dp row partials
   constexpr int UMASK = (BN / 4 >= 32) ? 31 : (BN / 4 - 1);  // staging swizzle (8-byte units)
   static_assert(TM >= 1 && TN >= 1 && A_PW >= 1 && B_PW >= 1, "tile config");
   static_assert((BM / RPB) % NW == 0 && (BN / RPB) % NW == 0, "DMA blocks must split across waves");
-  static_assert(BK == 64 || BQ8 == B_BF16, "fp8 weights use 64-wide k-tiles");
+  static_assert(BK == 64 || !W8, "fp8 weights with bf16 A use 64-wide k-tiles");
+  static_assert(!A8 || BK == 32, "fp8 A and B stages hold 64-byte rows");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN % 2 == 0), "SwiGLU forward pairs gate/up blocks");
   static_assert(BM * BN * 2 <= LDS_BYTES, "epilogue staging must fit the LDS ring");
   static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 6, "vmcnt range");
   static_assert(LDS_BYTES + RED_BYTES <= 160 * 1024, "LDS of one workgroup");
   static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
-  static_assert(!BQ8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
+  static_assert(!W8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
 
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES];
   float *sRed = (float *)(smem + LDS_BYTES);
@@ -318,9 +371,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   const int total = p.tile_off[p.E] * n_tiles;
   const int nb = gridDim.x;
   const int lb = (nb % 8 == 0) ? ((blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3)) : blockIdx.x;
-  const int nk_main = (p.K + BK - 1) / BK;
+  const int nk_main = (p.K + KPS - 1) / KPS;
   const int nk = nk_main + (p.kt + BK - 1) / BK;
-  const int nk_full = p.K / BK;  // full 64-wide k-tiles of the base product
+  const int nk_full = p.K / KPS;  // full k-tiles of the base product
   // DMA slot of this lane inside a 1 KB block (RPB rows): row lane/CPR,
   // physical chunk lane%CPR, holding logical chunk (lane%CPR) ^ chunk_swz(row).
   const int drow = lane / CPR, dch = lane % CPR;
@@ -340,18 +393,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // 32-bit byte offsets from wave-uniform bases (the host checks that every
     // operand spans less than 4 GiB).
     const char *abase = (const char *)p.a;
-    const char *bbase = BQ8 ? (const char *)p.b + (int64_t)e * p.b_es
-                            : (const char *)(p.b + (int64_t)e * p.b_es);
-    uint32_t aoff[A_PW], boff[BQ8 ? B_PW8 : B_PW];
+    const char *bbase = (W8 || A8) ? (const char *)p.b + (int64_t)e * p.b_es
+                                   : (const char *)(p.b + (int64_t)e * p.b_es);
+    uint32_t aoff[A_PW], boff[W8 ? B_PW8 : B_PW];
 #pragma unroll
     for (int i = 0; i < A_PW; ++i) {
       int m = m0 + (wave * A_PW + i) * RPB + drow;
       m = m < m_end ? m : m_end - 1;
       const uint32_t src = p.a_rows ? (uint32_t)p.a_rows[m] : (uint32_t)m;
       const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>((wave * A_PW + i) * RPB + drow));
-      aoff[i] = (src * (uint32_t)p.lda + ch * 8) * 2u;
+      aoff[i] = A8 ? src * (uint32_t)p.lda + ch * 16u : (src * (uint32_t)p.lda + ch * 8) * 2u;
     }
-    if (BQ8) {
+    if (W8) {
 #pragma unroll
       for (int i = 0; i < B_PW8; ++i) {
         const int r = (wave * B_PW8 + i) * 16 + (lane >> 2);
@@ -365,7 +418,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         const int r = (wave * B_PW + i) * RPB + drow;
         const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
         const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>(r));
-        boff[i] = ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
+        boff[i] = A8 ? (uint32_t)n * (uint32_t)p.ldb + ch * 16u
+                     : ((uint32_t)n * (uint32_t)p.ldb + ch * 8) * 2u;
       }
     }
     // fp8 weights with row scales: the scale of each B fragment row
@@ -373,9 +427,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       bsc[j] = 1.0f;
-      if (BQ8 == B_FP8_ROWSCALE)
+      if (BQ8 == B_FP8_ROWSCALE || (A8 && p.b_scale))
         bsc[j] = p.b_scale[(int64_t)e * p.bs_es +
                            b_source_row<EPI, BN>(wn * WTN + j * 32 + lrow, nt, p.N, p.F)];
+    }
+    // fp8 A and B: the row scale of each A fragment row (A source row)
+    float asc[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      asc[i] = 1.0f;
+      if (A8) {
+        int m = m0 + wm * WTM + i * 32 + lrow;
+        m = m < m_end ? m : m_end - 1;
+        asc[i] = p.a_scale[p.a_rows ? p.a_rows[m] : m];
+      }
     }
 
     // LoRA K-extension stages: offsets into Tl (same rows, not gathered) and L,
@@ -404,7 +469,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   do {                                                                                        \
     char *st_ = smem + ((ks) % STAGES) * STAGE_BYTES;                                         \
     if ((ks) < nk_full) {                                                                     \
-      if constexpr (BQ8 != B_BF16) {                                                          \
+      if constexpr (W8) {                                                                     \
         issue_stage_b8<A_PW, B_PW8, A_BYTES>(st_, wave, abase, bbase, aoff, boff,             \
                                              (uint32_t)((ks) * BK * 2), (uint32_t)((ks) * BK)); \
         if (BQ8 == B_FP8_KSCALE && wave == 0 && lane < BK / 4)                                \
@@ -449,7 +514,17 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // Full k-tiles of the base product: branch-free, fragments of step kk+1
     // are read while step kk multiplies.  (A separate loop keeps the
     // accumulators in one register assignment across iterations.)
-    if constexpr (BK == 32) {
+    if constexpr (A8) {
+      // fp8 activations x fp8 weights: one 32x32x64 MFMA step per block and
+      // stage (the per-row scales are applied in the epilogue).
+      for (int ks = 0; ks < nk_full; ++ks) {
+        ART_STAGE_IN(ks);
+        const char *st = smem + (ks % STAGES) * STAGE_BYTES;
+        i32x8 af[TM], bfv[TN];
+        load_frags_f8<TM, TN, WTM, WTN, A_BYTES>(st, wm, wn, lrow, lk, af, bfv);
+        mma_step_f8<TM, TN>(acc, af, bfv);
+      }
+    } else if constexpr (BK == 32) {
       // Two k-steps per stage.  The wait + barrier for stage ks+1 sits between
       // the two steps of stage ks: after it, every wave has finished reading
       // stage ks (its slot takes stage ks+STAGES) and stage ks+1 is visible, so
@@ -482,7 +557,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       // its first use (which would expose every LDS latency), so the wait
       // before a step's MFMAs only covers the previous group of reads.
 #define ART_FENCE() __builtin_amdgcn_sched_barrier(0)
-      if (BQ8) {
+      if (W8) {
         const float *ksc = (const float *)(st + A_BYTES + B_BYTES);
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 0, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 1, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
@@ -516,7 +591,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // Tail: a partial base k-tile and the LoRA K-extension tiles.  (With
     // BK = 32 the last full k-tile already brought stage nk_full in.)
     for (int ks = nk_full; ks < nk; ++ks) {
-      if (BK == 64 || nk_full == 0 || ks > nk_full) ART_STAGE_IN(ks);
+      if (BK == 64 || A8 || nk_full == 0 || ks > nk_full) ART_STAGE_IN(ks);
       const char *st = smem + (ks % STAGES) * STAGE_BYTES;
       const bool main = ks < nk_main;
       const int kb = (main ? ks : ks - nk_main) * BK;
@@ -525,6 +600,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       for (int kk = 0; kk < nkk; ++kk) {
         bf16x8 af[TM], bfv[TN];
         load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, kk, wm, wn, lrow, lk, af, bfv);
+        if (A8) {  // LoRA terms join the fp8 accumulators pre-divided by the row scales
+#pragma unroll
+          for (int i = 0; i < TM; ++i) af[i] = scale_frag(af[i], 1.0f / asc[i]);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) bfv[j] = scale_frag(bfv[j], 1.0f / bsc[j]);
+        }
         mma_step<TM, TN>(acc, af, bfv);
       }
     }
@@ -534,6 +615,19 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     barrier_nofence();  // every wave is done reading the ring: reuse it for staging
 
     // ------------------------------------------------------------ epilogue
+    if (A8) {  // acc[i][j][v] *= s_a[row] * s_b[column] (the fp8 operands' scales)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int nl = wn * WTN + j * 32 + 8 * (v / 4) + 4 * lk + (v % 4);
+          const float sb = p.b_scale ? p.b_scale[(int64_t)e * p.bs_es +
+                                                 b_source_row<EPI, BN>(nl, nt, p.N, p.F)]
+                                     : 1.0f;
+#pragma unroll
+          for (int i = 0; i < TM; ++i) acc[i][j][v] *= asc[i] * sb;
+        }
+    }
     // acc[i][j][v] is C[m][n] with m = wm*WTM + i*32 + lane%32 and
     // n = wn*WTN + j*32 + 8*(v/4) + 4*(lane/32) + v%4 (tile-local).
     uint2 *stg = (uint2 *)smem;  // staging tile, rows of BN bf16 in 8-byte units
@@ -807,6 +901,10 @@ static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, h
 template <int EPI>
 static int launch_fp8(int fmt, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
                       const char *what) {
+  if (fmt == B_FP8_AB) {  // fp8 x fp8: 64-byte rows (BK = 32 geometry), 4-stage rings
+    if (EPI == EPI_SWIGLU_BWD) return launch_nt<128, 256, 2, 4, 4, EPI, B_FP8_AB, 32>(p, seg, M, s, what);
+    return launch_nt<256, 256, 2, 4, 4, EPI, B_FP8_AB, 32>(p, seg, M, s, what);
+  }
   if (EPI == EPI_SWIGLU_BWD) {
     if (fmt == B_FP8_ROWSCALE) return launch_nt<128, 256, 2, 4, 2, EPI, B_FP8_ROWSCALE>(p, seg, M, s, what);
     return launch_nt<128, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
@@ -858,11 +956,24 @@ static int check_common(const void *a, int64_t lda, const void *b, int64_t ldb,
 }
 
 // fp8 weights: 64-wide k-tiles only (no partial k-tile), 16-byte rows and
-// scale rows (the per-k scales move in 16-byte chunks).
+// scale rows (the per-k scales move in 16-byte chunks).  AB_FP8 (fp8 A too):
+// A rows of lda bytes (% 16), a scale per A source row, optional per-row B
+// scales read element-wise.
 static int check_fp8(int32_t fmt, const void *b, int64_t ldb, const float *b_scale,
-                     int64_t bs_es, int32_t K, int32_t N, const char *who) {
-  ART_REQUIRE(fmt == ART_MOE_B_BF16 || fmt == ART_MOE_B_FP8_ROWSCALE || fmt == ART_MOE_B_FP8_KSCALE,
+                     int64_t bs_es, int32_t K, int32_t N, int64_t lda, const float *a_scale,
+                     const char *who) {
+  ART_REQUIRE(fmt == ART_MOE_B_BF16 || fmt == ART_MOE_B_FP8_ROWSCALE ||
+                  fmt == ART_MOE_B_FP8_KSCALE || fmt == ART_MOE_AB_FP8,
               "%s: unknown weight format %d", who, fmt);
+  if (fmt == ART_MOE_AB_FP8) {
+    ART_REQUIRE(K % 64 == 0, "%s: fp8 operands need K a multiple of 64 (K=%d)", who, K);
+    ART_REQUIRE(ldb % 16 == 0 && lda % 16 == 0,
+                "%s: fp8 operands need lda and ldb multiples of 16", who);
+    ART_REQUIRE(a_scale, "%s: fp8 A needs its row scales", who);
+    ART_REQUIRE(!b_scale || bs_es >= N, "%s: scale expert stride too small", who);
+    return ART_MOE_OK;
+  }
+  ART_REQUIRE(!a_scale, "%s: A row scales need fp8 A (ART_MOE_AB_FP8)", who);
   if (fmt == ART_MOE_B_BF16) return ART_MOE_OK;
   ART_REQUIRE(K % 64 == 0, "%s: fp8 weights need K a multiple of 64 (K=%d)", who, K);
   ART_REQUIRE(ldb % 16 == 0, "%s: fp8 weights need ldb a multiple of 16", who);
@@ -875,7 +986,7 @@ static int check_fp8(int32_t fmt, const void *b, int64_t ldb, const float *b_sca
 }
 
 extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
-                                    const void *b, int64_t ldb, int64_t b_estride,
+                                    const float *a_scale, const void *b, int64_t ldb, int64_t b_estride,
                                     const float *b_scale, int64_t bs_estride, int32_t b_format,
                                     const void *tl, int64_t ldt, const void *l, int64_t ldl,
                                     int64_t l_estride, int32_t kt, const int32_t *seg, int32_t E,
@@ -884,7 +995,7 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   clear_error();
   int rc = check_common(a, lda, b, ldb, seg, E, M, K, kt, tl, ldt, l, ldl, "grouped_gemm");
   if (rc) return rc;
-  rc = check_fp8(b_format, b, ldb, b_scale, bs_estride, K, N, "grouped_gemm");
+  rc = check_fp8(b_format, b, ldb, b_scale, bs_estride, K, N, lda, a_scale, "grouped_gemm");
   if (rc) return rc;
   ART_REQUIRE(N > 0 && N % 8 == 0 && c, "grouped_gemm: need N a positive multiple of 8 and an output");
   ART_REQUIRE(ldc >= N && ldc % 8 == 0 && aligned16(c),
@@ -893,7 +1004,7 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
               "grouped_gemm: one expert's B / L must span less than 4 GiB");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
-  p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
+  p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows; p.a_scale = a_scale;
   p.b = (const bf16 *)b; p.ldb = ldb; p.b_es = b_estride;
   p.b_scale = b_scale; p.bs_es = bs_estride;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
@@ -908,7 +1019,7 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
 }
 
 extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                                  const void *w1, const float *w1_scale, int32_t w1_format,
+                                  const float *a_scale, const void *w1, const float *w1_scale, int32_t w1_format,
                                   const void *tl, int64_t ldt, const void *l1,
                                   int32_t kt, const int32_t *seg, int32_t E, int64_t M, int32_t F,
                                   int32_t K, const float *row_prob, void *y1, void *h,
@@ -917,14 +1028,14 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
   int rc = check_common(a, lda, w1, K, seg, E, M, K, kt, tl, ldt, l1, kt, "fc1_swiglu");
   if (rc) return rc;
   ART_REQUIRE(w1_format != ART_MOE_B_FP8_KSCALE, "fc1_swiglu: fp8 W1 takes per-row scales");
-  rc = check_fp8(w1_format, w1, K, w1_scale, 2 * (int64_t)F, K, 2 * F, "fc1_swiglu");
+  rc = check_fp8(w1_format, w1, K, w1_scale, 2 * (int64_t)F, K, 2 * F, lda, a_scale, "fc1_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 64 == 0, "fc1_swiglu: F must be a positive multiple of 64 (F=%d)", F);
   ART_REQUIRE(row_prob && y1 && h, "fc1_swiglu: null pointer");
   ART_REQUIRE(aligned16(y1) && aligned16(h), "fc1_swiglu: outputs must be 16-byte aligned");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
-  p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
+  p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows; p.a_scale = a_scale;
   p.b = (const bf16 *)w1; p.ldb = K; p.b_es = (int64_t)2 * F * K;
   p.b_scale = w1_scale; p.bs_es = (int64_t)2 * F;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
@@ -940,7 +1051,7 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
 extern "C" int art_moe_dgrad_swiglu_parts(int32_t F) { return F > 0 ? (F + 127) / 128 : 0; }
 
 extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                                        const void *w2t, const float *w2_scale, int32_t w2_format,
+                                        const float *a_scale, const void *w2t, const float *w2_scale, int32_t w2_format,
                                         const void *tl, int64_t ldt,
                                         const void *l2, int32_t kt, const int32_t *seg, int32_t E,
                                         int64_t M, int32_t F, int32_t K, const void *y1,
@@ -951,16 +1062,17 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
   if (rc) return rc;
   ART_REQUIRE(w2_format != ART_MOE_B_FP8_ROWSCALE,
               "fc2_dgrad_swiglu: fp8 W2^T takes per-k scales (the FC2 output channels)");
-  rc = check_fp8(w2_format, w2t, K, w2_scale, K, K, F, "fc2_dgrad_swiglu");
+  rc = check_fp8(w2_format, w2t, K, w2_scale, w2_format == ART_MOE_AB_FP8 ? F : K, K, F, lda,
+                 a_scale, "fc2_dgrad_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 8 == 0, "fc2_dgrad_swiglu: F must be a positive multiple of 8 (F=%d)", F);
   ART_REQUIRE(y1 && row_prob && dy1 && dp_part, "fc2_dgrad_swiglu: null pointer");
   ART_REQUIRE(aligned16(y1) && aligned16(dy1), "fc2_dgrad_swiglu: y1/dy1 must be 16-byte aligned");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
-  p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows;
+  p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows; p.a_scale = a_scale;
   p.b = (const bf16 *)w2t; p.ldb = K; p.b_es = (int64_t)F * K;
-  p.b_scale = w2_scale; p.bs_es = K;
+  p.b_scale = w2_scale; p.bs_es = w2_format == ART_MOE_AB_FP8 ? F : K;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
   p.l = kt ? (const bf16 *)l2 : nullptr; p.ldl = kt; p.l_es = (int64_t)F * kt; p.kt = kt;
   p.E = E; p.N = F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;

@@ -1,0 +1,103 @@
+// Per-row OCP e4m3fn quantisation of bf16 activations: the A operand of the
+// fp8 x fp8 grouped products (ART_MOE_AB_FP8).
+//
+// Row m of the output is row rows[m] (or m) of src, optionally multiplied
+// column-wise by the per-expert column scales cs[e(m)][k] (e(m) the expert
+// segment holding m).  That folds a weight's per-k scales into the activation:
+// x W^T with W = q * s per k equals (x * s) q^T.  Each row is scaled by
+// s_row = amax / 448 (1 for an all-zero row), q = e4m3fn(v / s_row) rounded to
+// nearest even, and s_row is stored beside it; q * s_row reproduces v to fp8
+// precision.  Bandwidth-bound: one wavefront per row, two passes over the row
+// (the second from L1/L2), 16-byte loads, 8-byte stores.
+#include "common.h"
+
+namespace art {
+
+namespace {
+
+__device__ __forceinline__ float wave_absmax(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// 8 values of row (k .. k+7), times the column scales when given.
+__device__ __forceinline__ void row_chunk(const bf16 *x, const float *c, int k, float (&f)[8]) {
+  unpack8(*(const U4 *)(x + k), f);
+  if (c) {
+    const float4 c0 = *(const float4 *)(c + k), c1 = *(const float4 *)(c + k + 4);
+    f[0] *= c0.x; f[1] *= c0.y; f[2] *= c0.z; f[3] *= c0.w;
+    f[4] *= c1.x; f[5] *= c1.y; f[6] *= c1.z; f[7] *= c1.w;
+  }
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(256) void quant_rows_kernel(
+    const bf16 *__restrict__ src, int64_t lds, const int32_t *__restrict__ rows,
+    const int32_t *__restrict__ seg, int E, const float *__restrict__ cs, int64_t cs_es,
+    int64_t M, int K, uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ row_scale) {
+  const int lane = lane_id();
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const bf16 *x = src + (int64_t)(rows ? rows[m] : m) * lds;
+  const float *c = nullptr;
+  if (cs) {  // expert of row m: the last e with seg[e] <= m
+    int lo = 0, hi = E;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (seg[mid] <= m) lo = mid; else hi = mid;
+    }
+    c = cs + (int64_t)lo * cs_es;
+  }
+  float amax = 0.0f;
+  for (int k = lane * 8; k < K; k += kWave * 8) {
+    float f[8];
+    row_chunk(x, c, k, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  }
+  amax = wave_absmax(amax);
+  const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+  uint8_t *qr = q + m * ldq;
+  for (int k = lane * 8; k < K; k += kWave * 8) {
+    float f[8];
+    row_chunk(x, c, k, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = fminf(fmaxf(f[i] / s, -448.0f), 448.0f);
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], hi, true);
+    *(uint2 *)(qr + k) = make_uint2((unsigned)lo, (unsigned)hi);
+  }
+  if (lane == 0) row_scale[m] = s;
+}
+
+}  // namespace art
+
+using namespace art;
+
+extern "C" int art_moe_quantize_rows_fp8(const void *src, int64_t ld_src, const int32_t *rows,
+                                         const int32_t *seg, int32_t E, const float *col_scale,
+                                         int64_t cs_estride, int64_t M, int32_t K, void *q,
+                                         int64_t ldq, float *row_scale, void *stream) {
+  clear_error();
+  ART_REQUIRE(M >= 0 && K > 0 && K % 8 == 0, "quantize_rows_fp8: need M >= 0 and K %% 8 == 0 (K=%d)",
+              K);
+  if (M == 0) return ART_MOE_OK;
+  ART_REQUIRE(src && q && row_scale, "quantize_rows_fp8: null pointer");
+  ART_REQUIRE(ld_src >= K && ld_src % 8 == 0 && ((uintptr_t)src & 15) == 0,
+              "quantize_rows_fp8: src rows must be 16-byte aligned with ld_src >= K");
+  ART_REQUIRE(ldq >= K && ldq % 8 == 0 && ((uintptr_t)q & 7) == 0,
+              "quantize_rows_fp8: q rows must be 8-byte aligned with ldq >= K");
+  if (col_scale) {
+    ART_REQUIRE(seg && E >= 1, "quantize_rows_fp8: column scales need the segment offsets");
+    ART_REQUIRE(cs_estride >= K && cs_estride % 4 == 0 && ((uintptr_t)col_scale & 15) == 0,
+                "quantize_rows_fp8: column scales must be 16-byte aligned rows of >= K");
+  }
+  quant_rows_kernel<<<dim3((unsigned)((M + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      (const bf16 *)src, ld_src, rows, seg, E, col_scale, cs_estride, M, K, (uint8_t *)q, ldq,
+      row_scale);
+  return check_launch("quantize_rows_fp8");
+}

@@ -55,11 +55,15 @@ extern "C" {
 
 #define ART_MOE_SEG_NBM 5
 
-/* Weight storage of the grouped products (b_format / w*_format arguments):
- * bf16, or OCP fp8 e4m3fn with an fp32 scale per output row or per k. */
+/* Operand storage of the grouped products (b_format / w*_format arguments):
+ * bf16, or OCP fp8 e4m3fn weights with an fp32 scale per output row or per k
+ * (bf16 activations, W8A16); or ART_MOE_AB_FP8: fp8 e4m3fn weights AND
+ * activations (W8A8) on the fp8 MFMA, C = s_a[row] * s_b[n] * (A_q B_q^T)
+ * with a_scale per A source row and optional b_scale per B row (n). */
 #define ART_MOE_B_BF16 0
 #define ART_MOE_B_FP8_ROWSCALE 1
 #define ART_MOE_B_FP8_KSCALE 2
+#define ART_MOE_AB_FP8 3
 #define ART_MOE_SEG_LEN(E) ((1 + ART_MOE_SEG_NBM) * ((E) + 1))
 
 /* Library version, e.g. 100 for 0.1.0. */
@@ -163,11 +167,17 @@ int art_moe_combine(const void *y_perm, const int32_t *dest, const float *wgt,
  * ROWSCALE) or i = c (per k, KSCALE); the product uses bf16(q * scale) as
  * the weight, i.e. the dequantised weight.  fp8 needs K % 64 == 0,
  * ldb % 16 == 0 and 16-byte aligned scales with bs_estride % 4 == 0.
+ * ART_MOE_AB_FP8: A is fp8 e4m3fn too (lda in bytes, % 16) with fp32
+ * a_scale[row] per A source row (a_rows[m] or m); b_scale (nullable) per B
+ * row n.  The LoRA operands Tl, L stay bf16 and are divided in-kernel by the
+ * row scales so that they join the same accumulators.  a_scale must be null
+ * for the other formats.  (W8A8 has no reference counterpart: activation
+ * rounding to e4m3 costs ~2.7% relative error, see the fp8 tests.)
  * Replaces: TE GroupedLinear forward/dgrad (lora.py:1515-1521, 1559-1565),
  * QuACK varlen-M GEMMs (cute_grouped_lora_quack.py:257-298) and the
  * base + adapter add (lora.py:1529, 1571). */
 int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
-                         const void *b, int64_t ldb, int64_t b_estride,
+                         const float *a_scale, const void *b, int64_t ldb, int64_t b_estride,
                          const float *b_scale, int64_t bs_estride,
                          int32_t b_format, const void *tl, int64_t ldt, const void *l,
                          int64_t ldl, int64_t l_estride, int32_t kt,
@@ -181,11 +191,12 @@ int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
  * h[m, f] = silu(g) * u * row_prob[m] (bf16 [M][F]) where g = y1[m, f],
  * u = y1[m, F + f] rounded to bf16 first.  F % 64 == 0.
  * W1 is bf16 (w1_format ART_MOE_B_BF16) or fp8 with per-row scales
- * w1_scale [E][2F] (ART_MOE_B_FP8_ROWSCALE).
+ * w1_scale [E][2F] (ART_MOE_B_FP8_ROWSCALE, or ART_MOE_AB_FP8 with fp8 A
+ * and a_scale as in art_moe_grouped_gemm).
  * Replaces: MLPExpertsLinearFC1LoRA.forward (lora.py:1512-1529) followed by
  * weighted_bias_swiglu_impl (compile_workarounds.py:73-106). */
 int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                       const void *w1, const float *w1_scale, int32_t w1_format,
+                       const float *a_scale, const void *w1, const float *w1_scale, int32_t w1_format,
                        const void *tl, int64_t ldt,
                        const void *l1, int32_t kt, const int32_t *seg,
                        int32_t E, int64_t M, int32_t F, int32_t K,
@@ -203,11 +214,14 @@ int art_moe_dgrad_swiglu_parts(int32_t F);
  *   dp_part[i][m] = partial sums over f of dh * silu(g) * u
  *                   (i < art_moe_dgrad_swiglu_parts(F)).
  * W2T is bf16 (ART_MOE_B_BF16) or fp8 with the FC2 weight's per-output-row
- * scales w2_scale [E][K], which are per-k scales here (ART_MOE_B_FP8_KSCALE).
+ * scales w2_scale [E][K], which are per-k scales here (ART_MOE_B_FP8_KSCALE);
+ * with ART_MOE_AB_FP8, A is fp8 with a_scale per row and the per-k weight
+ * scales must already be folded into A (art_moe_quantize_rows_fp8 with
+ * col_scale); w2_scale is then an optional per-row (F) scale.
  * Replaces: TE GroupedLinear dgrad of FC2 + QuACK LoRA dgrad
  * (cute_grouped_lora_quack.py:394-410) + weighted_swiglu_back. */
 int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
-                             const void *w2t, const float *w2_scale,
+                             const float *a_scale, const void *w2t, const float *w2_scale,
                              int32_t w2_format, const void *tl, int64_t ldt,
                              const void *l2, int32_t kt, const int32_t *seg,
                              int32_t E, int64_t M, int32_t F, int32_t K,
@@ -325,6 +339,20 @@ typedef struct {
  * Replaces the rank padding / permute / cat copies of
  * cute_grouped_lora_quack.py:205-224, 350-353, 465-468. */
 int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *stream);
+
+/* Per-row OCP e4m3fn quantisation of bf16 rows, the A operand of the
+ * ART_MOE_AB_FP8 products: for m < M with v[k] = src[r][k] * cs[k],
+ * r = rows ? rows[m] : m and cs = col_scale ? col_scale + e(m)*cs_estride
+ * (e(m): the expert segment of seg holding m) : 1,
+ *   row_scale[m] = max_k |v[k]| / 448 (1 for an all-zero row),
+ *   q[m][k] = e4m3fn(v[k] / row_scale[m]) (round to nearest even).
+ * col_scale folds a weight's per-k scales into the activation (data-gradient
+ * products).  K % 8 == 0; src 16-byte aligned rows; q 8-byte aligned.
+ * No reference counterpart: the reference keeps activations in bf16. */
+int art_moe_quantize_rows_fp8(const void *src, int64_t ld_src, const int32_t *rows,
+                              const int32_t *seg, int32_t E, const float *col_scale,
+                              int64_t cs_estride, int64_t M, int32_t K, void *q, int64_t ldq,
+                              float *row_scale, void *stream);
 
 #ifdef __cplusplus
 }

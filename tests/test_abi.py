@@ -53,20 +53,32 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert b"E <= 1024" in lib.art_moe_last_error()
     rc = lib.art_moe_router_topk(null, 4, 8, 9, null, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
-    rc = lib.art_moe_grouped_gemm(null, 12, null, null, 12, 0, null, 0, 0, null, 0, null, 0, 0,
-                                  0, null, 4, 16, 32, 12, 1.0, null, 32, 0, null)
+    rc = lib.art_moe_grouped_gemm(null, 12, null, null, null, 12, 0, null, 0, 0, null, 0, null, 0,
+                                  0, 0, null, 4, 16, 32, 12, 1.0, null, 32, 0, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
     assert b"multiple of 16" in lib.art_moe_last_error()
-    rc = lib.art_moe_fc1_swiglu(null, 64, null, null, null, 0, null, 0, null, 0, null, 4, 16, 100,
-                                64, null, null, null, null)
+    rc = lib.art_moe_fc1_swiglu(null, 64, null, null, null, null, 0, null, 0, null, 0, null, 4, 16,
+                                100, 64, null, null, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
     # fp8 weights: K must be a multiple of 64 (checked before any pointer is used)
     buf = ctypes.create_string_buffer(4096 + 16)
     base = (ctypes.addressof(buf) + 15) // 16 * 16
-    rc = lib.art_moe_grouped_gemm(base, 48, null, base, 48, 0, base, 64, _lib.B_FP8_ROWSCALE,
+    rc = lib.art_moe_grouped_gemm(base, 48, null, null, base, 48, 0, base, 64, _lib.B_FP8_ROWSCALE,
                                   null, 0, null, 0, 0, 0, base, 4, 16, 32, 48, 1.0, base, 32, 0,
                                   null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"multiple of 64" in lib.art_moe_last_error()
+    # fp8 activations (W8A8): row scales required; A row scales only with fp8 A
+    rc = lib.art_moe_grouped_gemm(base, 64, null, null, base, 64, 0, null, 0, _lib.AB_FP8,
+                                  null, 0, null, 0, 0, 0, base, 4, 16, 32, 64, 1.0, base, 32, 0,
+                                  null)
+    assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"row scales" in lib.art_moe_last_error()
+    rc = lib.art_moe_grouped_gemm(base, 64, null, base, base, 64, 0, null, 0, _lib.B_BF16,
+                                  null, 0, null, 0, 0, 0, base, 4, 16, 32, 64, 1.0, base, 32, 0,
+                                  null)
+    assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"AB_FP8" in lib.art_moe_last_error()
+    rc = lib.art_moe_quantize_rows_fp8(base, 12, null, null, 0, null, 0, 4, 12, base, 12, base,
+                                       null)
+    assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"K % 8" in lib.art_moe_last_error()
     rc = lib.art_moe_permute(null, null, 4, 2, 12, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
     rc = lib.art_moe_grouped_wgrad(null, 64, null, null, 64, null, null, 4, 100, 64, 12, 1.0,

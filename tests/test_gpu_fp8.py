@@ -140,3 +140,115 @@ def test_layer_fp8_weights_c4_widths(device):
         errs["d" + n] = rel(lora[n].grad.cpu(), leaves[n].grad)
     print("  rel errs", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
     assert all(v < 2e-2 for v in errs.values()), errs
+
+
+# ----------------------------------------------------------------- W8A8
+# fp8 activations x fp8 weights on the f8f6f4 MFMA.  The quantiser must equal
+# torch's float8_e4m3fn conversion (round to nearest even) byte for byte; the
+# products must equal fp32 products of the dequantised fp8 operands (exact
+# products, fp32 sums: 1e-2 covers the sum order and the bf16 rounding of the
+# LoRA operands divided by the row scales).
+
+
+def _ref_quant(v):
+    """Per-row e4m3fn quantisation in torch (CPU, fp32): (q, scale)."""
+    amax = v.abs().amax(-1)
+    s = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = (v / s[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn)
+    return q, s
+
+
+@pytest.mark.parametrize("gather,cols", [(False, False), (True, False), (True, True)])
+def test_quantize_rows_fp8_matches_torch(device, gather, cols):
+    ops = _ops()
+    g = torch.Generator().manual_seed(7 + gather + 2 * cols)
+    t, k, e = 300, 512, 6
+    x = torch.randn(t, k, generator=g).to(torch.bfloat16)
+    x[5] = 0  # an all-zero row takes scale 1
+    m = 900 if gather else t
+    rows = torch.randint(0, t, (m,), generator=g, dtype=torch.int32) if gather else None
+    counts = _counts(e, m, seed=3)
+    seg = ops.segments_from_counts(counts, e, device)
+    cs = (torch.rand(e, k, generator=g) * 0.05 + 0.001) if cols else None
+    q, s = ops.quantize_rows_fp8(x.to(device), rows=rows.to(device) if gather else None,
+                                 seg=seg if cols else None,
+                                 col_scale=cs.to(device) if cols else None, m=m)
+    v = x.float()[rows.long()] if gather else x.float()
+    if cols:
+        ex = torch.repeat_interleave(torch.arange(e), torch.tensor(counts))
+        v = v * cs[ex]
+    qr, sr = _ref_quant(v)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+
+
+def _deq(q, s):
+    return q.float() * s.reshape(*s.shape, 1)
+
+
+@pytest.mark.parametrize("kt", [0, 32])
+def test_w8a8_products_match_dequantised_fp32(device, kt):
+    from art_amd.quant import quantize_fp8_rows, transpose_fp8
+    ops = _ops()
+    e, t, k8, h, f = 8, 1200, 3, 512, 256
+    m = t * k8
+    print(f"w8a8 products kt={kt}", flush=True)
+    g = torch.Generator().manual_seed(11 + kt)
+    counts = _counts(e, m, seed=5)
+    seg = ops.segments_from_counts(counts, e, device)
+    ex = torch.repeat_interleave(torch.arange(e), torch.tensor(counts))
+    rows = torch.randint(0, t, (m,), generator=g, dtype=torch.int32)
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    w1 = torch.randn(e, 2 * f, h, generator=g) * 0.02
+    w2 = torch.randn(e, h, f, generator=g) * 0.02
+    q1, s1 = quantize_fp8_rows(w1.to(device))
+    q2, s2 = quantize_fp8_rows(w2.to(device))
+    d1, d2 = _deq(q1.cpu(), s1.cpu()), _deq(q2.cpu(), s2.cpu())
+    lora = {}
+    if kt:
+        lora = dict(tl=(torch.randn(m, kt, generator=g) * 0.3).to(torch.bfloat16),
+                    l=(torch.randn(e, 2 * f, kt, generator=g) * 0.05).to(torch.bfloat16))
+
+    def lora_ref(n_rows):
+        if not kt:
+            return 0.0
+        return torch.cat([lora["tl"][ex == i].float() @ lora["l"][i, :n_rows].float().t()
+                          for i in range(e)], 0)
+
+    def rel(a, b):
+        return ((a.float().cpu() - b).norm() / b.norm()).item()
+
+    # FC1 forward: fp8 x (gathered, per-token scales) x W1 with row scales
+    xq, xs = ops.quantize_rows_fp8(x.to(device))
+    xd = _deq(xq.cpu(), xs.cpu())[rows.long()]
+    ref1 = torch.cat([xd[ex == i] @ d1[i].t() for i in range(e)], 0) + lora_ref(2 * f)
+    tl = lora["tl"].to(device) if kt else None
+    c = ops.grouped_gemm(xq, q1, seg, e, m=m, a_rows=rows.to(device), a_scale=xs, b_scale=s1,
+                         tl=tl, l=lora["l"].to(device) if kt else None)
+    assert rel(c, ref1) < 1e-2
+    prob = torch.rand(m, generator=g)
+    y1, hh = ops.fc1_swiglu(xq, q1, seg, e, prob.to(device), m=m, a_rows=rows.to(device),
+                            a_scale=xs, w1_scale=s1, tl=tl,
+                            l1=lora["l"].to(device) if kt else None)
+    assert rel(y1, ref1) < 1e-2
+    gg, uu = y1.cpu().float().chunk(2, dim=1)
+    assert rel(hh, torch.nn.functional.silu(gg) * uu * prob[:, None]) < 1e-2
+    # FC2 data gradient with the SwiGLU backward: the per-k (H) weight scales of
+    # W2^T folded into the gathered dy rows before quantisation
+    dy = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    dyq, dys = ops.quantize_rows_fp8(dy.to(device), rows=rows.to(device), seg=seg,
+                                     col_scale=s2.reshape(e, h).contiguous(), m=m)
+    dyd = _deq(dyq.cpu(), dys.cpu())
+    l2 = lora["l"][:, :f].contiguous() if kt else None
+    dh_ref = torch.cat([dyd[ex == i] @ q2.cpu().float()[i] for i in range(e)], 0)
+    if kt:
+        dh_ref = dh_ref + torch.cat([lora["tl"][ex == i].float() @ l2[i].float().t()
+                                     for i in range(e)], 0)
+    dy1, dp = ops.fc2_dgrad_swiglu(dyq, transpose_fp8(q2), seg, e, y1, prob.to(device), m=m,
+                                   a_scale=dys, tl=tl, l2=l2.to(device) if kt else None)
+    y1f = y1.cpu().float().requires_grad_()
+    p = prob.clone().requires_grad_()
+    a_, b_ = y1f.chunk(2, dim=1)
+    (torch.nn.functional.silu(a_) * b_ * p[:, None]).backward(dh_ref)
+    assert rel(dy1, y1f.grad) < 1e-2
+    assert rel(dp.sum(0), p.grad) < 1e-2
