@@ -30,6 +30,7 @@ for _p in (REPO, REPO / "art-mlx_amd"):
 
 METRIC = "MoE-LoRA layer tokens/sec fwd+bwd (Qwen3-30B-A3B shape, 1 GPU); % MFMA/HBM peak"
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
 
@@ -37,7 +38,7 @@ NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
 GEMM_OPS = ("grouped_gemm", "fc1_swiglu", "fc2_dgrad_swiglu", "grouped_wgrad")
 HBM_OPS = ("router_topk", "router_replay", "dispatch_plan", "combine", "router_backward",
            "permute", "transpose_into", "segments_from_counts", "pack", "router_lora_apply",
-           "router_lora_grad")
+           "router_lora_grad", "quantize_rows_fp8")
 
 
 class OpTimer:
@@ -80,7 +81,7 @@ class OpTimer:
         return tot, cnt
 
 
-def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0):
+def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0, w8a8: bool = False):
     import torch
 
     from art_amd import ops
@@ -94,7 +95,7 @@ def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0):
         q1, s1 = quantize_fp8_rows(inp.w1)
         q2, s2 = quantize_fp8_rows(inp.w2)
         inp.w1 = inp.w2 = None
-        base = moe_layer.FrozenExperts.build_fp8(inp.w_r, q1, s1, q2, s2)
+        base = moe_layer.FrozenExperts.build_fp8(inp.w_r, q1, s1, q2, s2, act_fp8=w8a8)
     else:
         base = moe_layer.FrozenExperts.build(inp.w_r, inp.w1, inp.w2)
     names = NAMES + (("a_r", "b_r") if cfg.router_r else ())
@@ -207,6 +208,9 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=1024)
     ap.add_argument("--cpu-iters", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--w8a8", action="store_true",
+                    help="fp8 configs: fp8 activations too, base products on the fp8 MFMA "
+                         "(opt-in mode with its own tolerance; default W8A16 keeps the bf16 bar)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (profiler counter calibration)")
     args = ap.parse_args()
@@ -221,7 +225,11 @@ def main():
 
     from art_amd.workloads import CONFIGS
     cfg = CONFIGS[args.config]
-    ms, tot, cnt = gpu_bench(cfg, args.steps, args.warmup)
+    if args.w8a8 and not cfg.fp8:
+        print(f"--w8a8 needs an fp8-weight config (C4), not {cfg.name}", file=sys.stderr)
+        sys.exit(2)
+    ms, tot, cnt = gpu_bench(cfg, args.steps, args.warmup, w8a8=args.w8a8)
+    peak = PEAK_FP8_TFLOPS if args.w8a8 else PEAK_BF16_TFLOPS
     flops = cfg.flops_fwd_bwd()
     tokens_per_s = cfg.T / (ms / 1e3)
 
@@ -251,22 +259,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8 e4m3fn (W8A8 base products), bf16 LoRA" if args.w8a8 else "bf16",
         "data": "synthetic (seeded: x~N(0,1), W_r~N(0,1/H), frozen base W~N(0,0.02), LoRA A,B~N(0,0.01))",
         "config": {"workload": f"{cfg.name}: {cfg.note}, layer fwd+bwd", "T": cfg.T, "H": h,
                    "E": cfg.E, "k": cfg.k, "F": f, "r": r, "alpha": cfg.alpha,
                    "routing": "replay Zipf(1.2)" if cfg.replay else "top-k softmax (renormalised)",
                    "router_lora_rank": cfg.router_r,
-                   "base_weights": ("fp8 e4m3fn + per-row fp32 scale, dequantised to bf16 in the "
-                                    "product (bf16 MFMA)") if cfg.fp8 else "bf16",
+                   "base_weights": (("fp8 e4m3fn + per-row fp32 scale; activations quantised "
+                                     "to e4m3fn per row, fp8 MFMA (W8A8)") if args.w8a8 else
+                                    ("fp8 e4m3fn + per-row fp32 scale, dequantised to bf16 in the "
+                                     "product (bf16 MFMA)") if cfg.fp8 else "bf16"),
                    "lora_grads": "fp32 main_grad accumulation" if cfg.router_r else "bf16 (param dtype)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd)",
-                     "achieved": round(fc1_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(fc1_tflops / PEAK_BF16_TFLOPS, 4),
+                     "achieved": round(fc1_tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(fc1_tflops / peak, 4),
                      "traffic": measured_traffic(cfg.name),
                      "flops_per_launch": fc1_flops, "avg_launch_ms": round(fc1_ms, 4)},
-        "gemm_mfma_frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "gemm_mfma_frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / peak, 4),
         "gemm_ms_per_step": round(gemm_ms, 4),
         "bandwidth_ops_ms_per_step": round(hbm_ms, 4),
         "combine_hbm_frac": round(comb_bytes / (comb_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if comb_ms else None,
