@@ -219,7 +219,7 @@ __global__ __launch_bounds__(1024) void segments_kernel(const CT *__restrict__ c
       v = c;
     } else {
       // row-tile heights 64, 128, 192, 256 and the 2048-row wgrad chunk
-      const int bm = b == ART_MOE_SEG_NBM ? 2048 : 64 * b;
+      const int bm = b == ART_MOE_SEG_NBM ? ART_MOE_WGRAD_CHUNK : 64 * b;
       v = (c + bm - 1) / bm;
     }
     int total;

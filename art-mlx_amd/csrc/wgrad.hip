@@ -31,7 +31,7 @@ namespace art {
 
 constexpr int kWgBK = 64;          // segment rows per main-loop step
 constexpr int kWgBP = 128;         // P extent of a workgroup tile
-constexpr int kWgChunkRows = 2048; // rows per chunk: BM of the segment table's last tile row
+constexpr int kWgChunkRows = ART_MOE_WGRAD_CHUNK;  // rows per chunk: BM of the segment table's last tile row
 constexpr int kWgChunkSegRow = ART_MOE_SEG_NBM;  // that row's index in the table
 
 struct WArgs {
@@ -237,10 +237,20 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WArgs a) {
   for (int t = threadIdx.x; t < kWgBP * BQ; t += 256) {
     const int pl = t / BQ, ql = t - pl * BQ;
     if (p0 + pl >= a.P || q0 + ql >= a.Q) continue;
+    // partials of 8 chunks are loaded before they are added (same chunk order
+    // as a plain loop: the sum is identical, the loads overlap)
+    const size_t cstride = (size_t)a.n_pt * a.n_qt * (kWgBP * BQ);
+    const float *src = a.ws + (((size_t)c0 * a.n_pt + blockIdx.y) * a.n_qt + blockIdx.z) *
+                                  (size_t)(kWgBP * BQ) + t;
     float s = 0.0f;
-    for (int cc = 0; cc < nce; ++cc)
-      s += a.ws[(((size_t)(c0 + cc) * a.n_pt + blockIdx.y) * a.n_qt + blockIdx.z) *
-                    (size_t)(kWgBP * BQ) + t];
+    for (int cb = 0; cb < nce; cb += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = cb + u < nce ? src[(size_t)(cb + u) * cstride] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (cb + u < nce) s += v[u];
+    }
     wg_store(a, e, p0 + pl, q0 + ql, s);
   }
 }

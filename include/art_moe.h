@@ -54,6 +54,11 @@ extern "C" {
 #define ART_MOE_ERR_HIP (-3)
 
 #define ART_MOE_SEG_NBM 5
+/* Row chunk of the segmented weight-gradient products (the last tile height
+ * of the segment table). */
+#ifndef ART_MOE_WGRAD_CHUNK
+#define ART_MOE_WGRAD_CHUNK 2048
+#endif
 
 /* Operand storage of the grouped products (b_format / w*_format arguments):
  * bf16, or OCP fp8 e4m3fn weights with an fp32 scale per output row or per k
