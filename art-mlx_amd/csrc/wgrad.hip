@@ -9,28 +9,38 @@
 //
 // Work split: a segment is cut into chunks of kWgChunkRows rows (the segment
 // table's last tile row counts them per expert); one workgroup owns one
-// 128 x BQ output tile of one chunk.  A chunk that is its expert's only one
+// wg_bp(BQ) x BQ output tile of one chunk.  A chunk that is its expert's only one
 // writes the output directly; chunks of longer segments write fp32 partial
 // tiles to the caller's workspace and a second kernel sums them in chunk
 // order.  Every output element is therefore one fixed-order fp32 sum
 // (deterministic, no atomics) while a heavily loaded expert (replayed Zipf
 // routes) is spread over several workgroups.
 //
-// Main loop per 64-row step: the next step's rows are loaded into registers
-// (16-byte loads, gathered through the row maps) while the MFMAs consume the
-// current step from LDS.  The MFMA operands need 8 consecutive rows per lane,
-// so rows are transposed on the way into LDS: two rows (m, m+1) are packed
-// into 32-bit words at [p][m] (row pitch 128 bytes = 64 rows m), and operand
-// fragments are single 16-byte LDS reads.  The 16-byte slot of a chunk is
-// XOR-swizzled with bits of the row index so that the 16 lanes of an operand
-// read cover all 64 banks and the transposing writes conflict at most 2-way.
+// Main loop: the 64-row steps of a chunk stream through a kWgStages-deep LDS
+// ring by global_load_lds DMA (16 bytes per lane, rows gathered through the
+// row maps, whose entries for the chunk are staged in LDS first so that no DMA
+// address waits on a global load), so several steps are in flight per
+// workgroup without holding them in registers.  Rows stay row-major in LDS;
+// the MFMA operands need 8 consecutive rows per lane (k = the segment row),
+// so each fragment is gathered with 8 16-bit LDS reads from rows m .. m+7 of
+// one column.  The 16-byte chunks of a row are XOR-swizzled by bits 3-4 of
+// the row index, which puts the four 16-lane groups of a read (rows m, m+8,
+// m+16, m+24; 16 consecutive columns) on distinct banks for rows of >= 8
+// chunks.  Rows past the chunk are DMA'd from its last row (valid memory) and
+// zeroed in the fragments of the last step.
 // MFMA: v_mfma_f32_16x16x32_bf16 (ranks of 16 waste nothing).
+#include <type_traits>
+
 #include "common.h"
 
 namespace art {
 
 constexpr int kWgBK = 64;          // segment rows per main-loop step
-constexpr int kWgBP = 128;         // P extent of a workgroup tile
+constexpr int kWgStages = 3;       // LDS ring depth
+// P extent of a workgroup tile for a Q tile of BQ: wide Q tiles (ranks >= 64)
+// take 256 P columns and 8 waves (half the re-reads of the R operand across P
+// tiles), narrow ones 128 columns and 4 waves (two workgroups per CU).
+constexpr int wg_bp(int bq) { return bq >= 64 ? 256 : 128; }
 constexpr int kWgChunkRows = ART_MOE_WGRAD_CHUNK;  // rows per chunk: BM of the segment table's last tile row
 constexpr int kWgChunkSegRow = ART_MOE_SEG_NBM;  // that row's index in the table
 
@@ -54,12 +64,6 @@ struct WArgs {
   int n_pt, n_qt;
 };
 
-// Byte offset in an LDS operand tile of the 16-byte chunk c (rows m = 8c..8c+7)
-// of row `row` (a p or q index).
-__device__ __forceinline__ int wg_off(int row, int c) {
-  return row * 128 + ((c ^ ((row >> 1) ^ (row >> 4)) & 7) << 4);
-}
-
 __device__ __forceinline__ void wg_store(const WArgs &a, int e, int p, int q, float acc) {
   const bool second = a.out2 != nullptr && q >= a.q_split;
   void *base = second ? a.out2 : a.out;
@@ -75,60 +79,55 @@ __device__ __forceinline__ void wg_store(const WArgs &a, int e, int p, int q, fl
   }
 }
 
-// 32-bit word holding element j of row m (low half) and of row m+1 (high half)
-__device__ __forceinline__ uint32_t pair_word(const U4 &a, const U4 &b, int j) {
-  const uint32_t wa = j < 2 ? a.x : j < 4 ? a.y : j < 6 ? a.z : a.w;
-  const uint32_t wb = j < 2 ? b.x : j < 4 ? b.y : j < 6 ? b.z : b.w;
-  return (j & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+typedef __attribute__((address_space(3))) void *wg_lds_ptr;
+
+// 16-byte chunk c of LDS row m (NCH chunks per row) sits at this physical chunk.
+template <int NCH>
+__device__ __forceinline__ int wg_chunk(int m, int c) {
+  return (c ^ (((m >> 3) & 3) << 1)) & (NCH - 1);
 }
 
-// Rows [mb, mb+64) x columns [c0, c0 + 8*NC) of a row-major operand: NPAIR
-// (row pair, 8-column chunk) items per thread, consecutive threads on
-// consecutive chunks of a row (coalesced).
-template <int NC, int NPAIR>
-__device__ __forceinline__ void wg_load(U4 (&v)[NPAIR][2], const bf16 *base, int64_t ld,
-                                        const int32_t *rows, int mb, int m_end, int c0, int ncols) {
+// Byte offset of element (m, col) in a swizzled row-major LDS tile.
+template <int NCH>
+__device__ __forceinline__ int wg_eoff(int m, int col) {
+  return m * (NCH * 16) + (wg_chunk<NCH>(m, col >> 3) << 4) + ((col & 7) << 1);
+}
+
+// Operand fragment of one 16x16x32 MFMA: 8 consecutive rows m0 + 8*(lane/16)
+// .. +7 of column col (lane%16 chosen by the caller), rows >= mlim as zero.
+template <int NCH, bool MASK>
+__device__ __forceinline__ bf16x8 wg_frag(const char *tile, int mb, int col, int mlim) {
+  uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < NPAIR; ++i) {
-    const int id = (int)threadIdx.x + 256 * i;
-    const int cc = id % NC, rp = id / NC;
-    const int col = c0 + cc * 8;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int m = mb + 2 * rp + h;
-      v[i][h] = U4{0u, 0u, 0u, 0u};
-      if (rp < kWgBK / 2 && m < m_end && col < ncols) {
-        const int64_t src = rows ? (int64_t)rows[m] : (int64_t)m;
-        v[i][h] = *(const U4 *)(base + src * ld + col);
-      }
+  for (int t = 0; t < 8; t += 2) {
+    uint32_t lo = *(const unsigned short *)(tile + wg_eoff<NCH>(mb + t, col));
+    uint32_t hi = *(const unsigned short *)(tile + wg_eoff<NCH>(mb + t + 1, col));
+    if (MASK) {
+      lo = mb + t < mlim ? lo : 0u;
+      hi = mb + t + 1 < mlim ? hi : 0u;
     }
+    w[t >> 1] = lo | (hi << 16);
   }
-}
-
-template <int NC, int NPAIR>
-__device__ __forceinline__ void wg_stash(const U4 (&v)[NPAIR][2], char *lds) {
-#pragma unroll
-  for (int i = 0; i < NPAIR; ++i) {
-    const int id = (int)threadIdx.x + 256 * i;
-    const int cc = id % NC, rp = id / NC;
-    if (rp >= kWgBK / 2) continue;
-    const int mm = 2 * rp;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *(uint32_t *)(lds + wg_off(cc * 8 + j, mm >> 3) + ((mm & 7) << 1)) =
-          pair_word(v[i][0], v[i][1], j);
-  }
+  bf16x8 v;
+  __builtin_memcpy(&v, w, 16);
+  return v;
 }
 
 // WP x WQ waves; each wave owns TP x TQ blocks of 16x16 outputs.
 template <int BQ, int WP, int WQ, int TP, int TQ>
-__global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
-  static_assert(WP * WQ == 4 && WP * TP * 16 == kWgBP && WQ * TQ * 16 == BQ, "tile");
-  constexpr int NCL = kWgBP / 8, NCR = BQ / 8;                    // 8-column chunks per row
-  constexpr int NPL = (NCL * kWgBK / 2 + 255) / 256;              // pair items per thread
-  constexpr int NPR = (NCR * kWgBK / 2 + 255) / 256;
-  constexpr int BUF = (kWgBP + BQ) * 128;                         // bytes per LDS buffer
-  __shared__ __attribute__((aligned(16))) char lds[2 * BUF];
+__global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
+  constexpr int kWgBP = wg_bp(BQ), NW = WP * WQ, kWgThreads = NW * 64;
+  static_assert(WP * TP * 16 == kWgBP && WQ * TQ * 16 == BQ, "tile");
+  constexpr int NCL = kWgBP / 8, NCR = BQ / 8;  // 16-byte chunks per L / R row
+  constexpr int L_BYTES = kWgBK * kWgBP * 2, R_BYTES = kWgBK * BQ * 2;
+  constexpr int STAGE = L_BYTES + R_BYTES;
+  constexpr int LI = L_BYTES / 1024 / NW;                 // L DMA instructions per wave
+  constexpr int RI = R_BYTES >= 1024 * NW ? R_BYTES / 1024 / NW : 1;
+  constexpr int R_LANES = R_BYTES >= 1024 * NW ? 64 : R_BYTES / 16 / NW;  // active lanes
+  constexpr int G = LI + RI;                              // DMA instructions per stage
+  static_assert(LI >= 1 && R_LANES >= 1 && RI * R_LANES * 16 * NW == R_BYTES, "DMA split");
+  __shared__ __attribute__((aligned(16))) char lds[kWgStages * STAGE];
+  __shared__ int32_t lrow_s[kWgChunkRows], rrow_s[kWgChunkRows];
 
   // 1-D grid, XCD-aware: workgroups are dispatched round-robin over the 8
   // XCDs, so the tiles of chunk c all go to XCD c % 8, back to back, and
@@ -149,57 +148,101 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
   const int nce = cpre[e + 1] - cpre[e];
   const int m0 = a.seg[e] + (c - cpre[e]) * kWgChunkRows;
   const int m1 = min(a.seg[e + 1], m0 + kWgChunkRows);
+  const int nrows = m1 - m0;  // >= 1
   const int p0 = ty * kWgBP, q0 = tz * BQ;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wp = wave % WP, wq = wave / WP;
   const int l16 = lane & 15, g4 = lane >> 4;
+
+  // the chunk's source rows, staged once
+  for (int i = tid; i < nrows; i += kWgThreads) {
+    lrow_s[i] = a.l_rows ? a.l_rows[m0 + i] : m0 + i;
+    rrow_s[i] = a.r_rows ? a.r_rows[m0 + i] : m0 + i;
+  }
+  __syncthreads();
+
+  // DMA slots of this lane: L instruction i covers rows (wave*LI + i) * RPI_L +
+  // lane / NCL of a stage (RPI_L = 1024 / (NCL*16) rows per instruction);
+  // R instruction i covers bytes ((wave*RI + i) * R_LANES + lane) * 16.
+  const char *lbase = (const char *)a.l;
+  const char *rbase = (const char *)a.r;
+  auto issue = [&](int ks) __attribute__((always_inline)) {
+    char *st = lds + (ks % kWgStages) * STAGE;
+    const int mb = ks * kWgBK;
+#pragma unroll
+    for (int i = 0; i < LI; ++i) {
+      const int off = ((wave * LI + i) * 64 + lane) * 16;
+      const int rl = off / (NCL * 16), pc = (off / 16) % NCL;
+      int m = mb + rl;
+      m = m < nrows ? m : nrows - 1;
+      int col = p0 + ((pc ^ (((rl >> 3) & 3) << 1)) & (NCL - 1)) * 8;
+      col = col < a.P ? col : a.P - 8;
+      const char *g = lbase + ((int64_t)lrow_s[m] * a.ldl + col) * 2;
+      __builtin_amdgcn_global_load_lds(g, (wg_lds_ptr)(st + (wave * LI + i) * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+      if (lane < R_LANES) {
+        const int off = ((wave * RI + i) * R_LANES + lane) * 16;
+        const int rl = off / (NCR * 16), pc = (off / 16) % NCR;
+        int m = mb + rl;
+        m = m < nrows ? m : nrows - 1;
+        int col = q0 + ((pc ^ (((rl >> 3) & 3) << 1)) & (NCR - 1)) * 8;
+        col = col < a.Q ? col : a.Q - 8;
+        const char *g = rbase + ((int64_t)rrow_s[m] * a.ldr + col) * 2;
+        __builtin_amdgcn_global_load_lds(
+            g, (wg_lds_ptr)(st + L_BYTES + (wave * RI + i) * R_LANES * 16), 16, 0, 0);
+      }
+    }
+  };
 
   f32x4 acc[TP][TQ];
 #pragma unroll
   for (int i = 0; i < TP; ++i)
 #pragma unroll
-    for (int j = 0; j < TQ; ++j)
+    for (int jj = 0; jj < TQ; ++jj)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.0f;
+      for (int v = 0; v < 4; ++v) acc[i][jj][v] = 0.0f;
 
-  U4 vl[NPL][2], vr[NPR][2];
-  const int nk = (m1 - m0 + kWgBK - 1) / kWgBK;
-  wg_load<NCL, NPL>(vl, a.l, a.ldl, a.l_rows, m0, m1, p0, a.P);
-  wg_load<NCR, NPR>(vr, a.r, a.ldr, a.r_rows, m0, m1, q0, a.Q);
-  wg_stash<NCL, NPL>(vl, lds);
-  wg_stash<NCR, NPR>(vr, lds + kWgBP * 128);
-  __syncthreads();
-  for (int ks = 0; ks < nk; ++ks) {
-    const bool more = ks + 1 < nk;
-    if (more) {  // next step's rows in flight during this step's MFMAs
-      const int mb = m0 + (ks + 1) * kWgBK;
-      wg_load<NCL, NPL>(vl, a.l, a.ldl, a.l_rows, mb, m1, p0, a.P);
-      wg_load<NCR, NPR>(vr, a.r, a.ldr, a.r_rows, mb, m1, q0, a.Q);
-    }
-    const char *bl = lds + (ks & 1) * BUF;
-    const char *br = bl + kWgBP * 128;
+  auto compute = [&](int ks, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const char *tl = lds + (ks % kWgStages) * STAGE;
+    const char *tr = tl + L_BYTES;
+    const int mlim = nrows - ks * kWgBK;
 #pragma unroll
     for (int kk = 0; kk < kWgBK / 32; ++kk) {
-      const int cidx = kk * 4 + g4;  // lanes 16g..16g+15 take rows m = 32kk + 8g .. +7
+      const int mb = kk * 32 + 8 * g4;
       bf16x8 af[TP], bq[TQ];
 #pragma unroll
       for (int i = 0; i < TP; ++i)
-        af[i] = *(const bf16x8 *)(bl + wg_off(wp * TP * 16 + i * 16 + l16, cidx));
+        af[i] = wg_frag<NCL, MASK>(tl, mb, wp * TP * 16 + i * 16 + l16, mlim);
 #pragma unroll
-      for (int j = 0; j < TQ; ++j)
-        bq[j] = *(const bf16x8 *)(br + wg_off(wq * TQ * 16 + j * 16 + l16, cidx));
+      for (int jj = 0; jj < TQ; ++jj)
+        bq[jj] = wg_frag<NCR, MASK>(tr, mb, wq * TQ * 16 + jj * 16 + l16, mlim);
 #pragma unroll
       for (int i = 0; i < TP; ++i)
 #pragma unroll
-        for (int j = 0; j < TQ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bq[j], acc[i][j], 0, 0, 0);
+        for (int jj = 0; jj < TQ; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bq[jj], acc[i][jj], 0, 0, 0);
     }
-    if (more) {  // the other buffer: its last readers passed the previous barrier
-      char *nb = lds + ((ks + 1) & 1) * BUF;
-      wg_stash<NCL, NPL>(vl, nb);
-      wg_stash<NCR, NPR>(vr, nb + kWgBP * 128);
-    }
-    __syncthreads();
+  };
+
+  const int nk = (nrows + kWgBK - 1) / kWgBK;
+#pragma unroll
+  for (int s = 0; s < kWgStages - 1; ++s)
+    if (s < nk) issue(s);
+  for (int ks = 0; ks < nk; ++ks) {
+    // stage ks landed (at most kWgStages-2 later stages in flight), then the
+    // slot of stage ks-1 is free for stage ks+kWgStages-1
+    const int pend = (nk - 1 - ks) < (kWgStages - 2) ? (nk - 1 - ks) : (kWgStages - 2);
+    if (pend >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(G) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (ks + kWgStages - 1 < nk) issue(ks + kWgStages - 1);
+    if (ks == nk - 1 && (nrows & (kWgBK - 1)))
+      compute(ks, std::true_type{});
+    else
+      compute(ks, std::false_type{});
   }
 
   // Accumulator element v of a 16x16 block: row 4*(lane/16) + v, column lane%16.
@@ -211,15 +254,15 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
 #pragma unroll
   for (int i = 0; i < TP; ++i)
 #pragma unroll
-    for (int j = 0; j < TQ; ++j)
+    for (int jj = 0; jj < TQ; ++jj)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int pl = wp * TP * 16 + i * 16 + g4 * 4 + v;
-        const int ql = wq * TQ * 16 + j * 16 + l16;
+        const int ql = wq * TQ * 16 + jj * 16 + l16;
         if (part) {
-          part[pl * BQ + ql] = acc[i][j][v];
+          part[pl * BQ + ql] = acc[i][jj][v];
         } else if (p0 + pl < a.P && q0 + ql < a.Q) {
-          wg_store(a, e, p0 + pl, q0 + ql, acc[i][j][v]);
+          wg_store(a, e, p0 + pl, q0 + ql, acc[i][jj][v]);
         }
       }
 }
@@ -228,6 +271,7 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const WArgs a) {
 // summed in chunk order (no chunk: zero).  One workgroup per (expert, tile).
 template <int BQ>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WArgs a) {
+  constexpr int kWgBP = wg_bp(BQ);
   const int e = blockIdx.x;
   const int32_t *cpre = a.seg + kWgChunkSegRow * (a.E + 1);
   const int c0 = cpre[e], nce = cpre[e + 1] - c0;
@@ -263,13 +307,13 @@ static int64_t wgrad_max_chunks(int64_t M, int E) {
 
 template <int BQ, int WP, int WQ, int TP, int TQ>
 static int launch_wgrad(WArgs a, int64_t M, hipStream_t s) {
-  a.n_pt = (a.P + kWgBP - 1) / kWgBP;
+  a.n_pt = (a.P + wg_bp(BQ) - 1) / wg_bp(BQ);
   a.n_qt = (a.Q + BQ - 1) / BQ;
   if (M > 0) {
     const int64_t groups = (wgrad_max_chunks(M, a.E) + 7) / 8;  // chunk groups of 8 (one per XCD)
     const int64_t blocks = groups * 8 * a.n_pt * a.n_qt;
     ART_REQUIRE(blocks < (int64_t)1 << 31, "grouped_wgrad: too many tiles");
-    wgrad_kernel<BQ, WP, WQ, TP, TQ><<<dim3((unsigned)blocks), 256, 0, s>>>(a);
+    wgrad_kernel<BQ, WP, WQ, TP, TQ><<<dim3((unsigned)blocks), WP * WQ * 64, 0, s>>>(a);
     if (int rc = check_launch("grouped_wgrad")) return rc;
   }
   wgrad_reduce_kernel<BQ><<<dim3((unsigned)a.E, a.n_pt, a.n_qt), 256, 0, s>>>(a);
@@ -282,9 +326,9 @@ using namespace art;
 
 extern "C" size_t art_moe_wgrad_workspace_bytes(int64_t M, int32_t E, int32_t P, int32_t Q) {
   if (M <= kWgChunkRows || E <= 0 || P <= 0 || Q <= 0) return 0;  // no segment spans two chunks
-  const int bq = wgrad_bq(Q);
-  return (size_t)wgrad_max_chunks(M, E) * ((P + kWgBP - 1) / kWgBP) * ((Q + bq - 1) / bq) *
-         kWgBP * bq * sizeof(float);
+  const int bq = wgrad_bq(Q), bp = wg_bp(bq);
+  return (size_t)wgrad_max_chunks(M, E) * ((P + bp - 1) / bp) * ((Q + bq - 1) / bq) * bp * bq *
+         sizeof(float);
 }
 
 extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
@@ -324,7 +368,7 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   switch (wgrad_bq(Q)) {
     case 16: return launch_wgrad<16, 4, 1, 2, 1>(a, M, s);
     case 32: return launch_wgrad<32, 4, 1, 2, 2>(a, M, s);
-    case 64: return launch_wgrad<64, 2, 2, 4, 2>(a, M, s);
-    default: return launch_wgrad<128, 2, 2, 4, 4>(a, M, s);
+    case 64: return launch_wgrad<64, 4, 2, 4, 2>(a, M, s);
+    default: return launch_wgrad<128, 4, 2, 4, 4>(a, M, s);
   }
 }
