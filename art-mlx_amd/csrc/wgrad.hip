@@ -21,13 +21,15 @@
 // row maps, whose entries for the chunk are staged in LDS first so that no DMA
 // address waits on a global load), so several steps are in flight per
 // workgroup without holding them in registers.  Rows stay row-major in LDS;
-// the MFMA operands need 8 consecutive rows per lane (k = the segment row),
-// so each fragment is gathered with 8 16-bit LDS reads from rows m .. m+7 of
-// one column.  The 16-byte chunks of a row are XOR-swizzled by bits 3-4 of
-// the row index, which puts the four 16-lane groups of a read (rows m, m+8,
-// m+16, m+24; 16 consecutive columns) on distinct banks for rows of >= 8
-// chunks.  Rows past the chunk are DMA'd from its last row (valid memory) and
-// zeroed in the fragments of the last step.
+// the MFMA operands need 8 consecutive rows per lane (k = the segment row), and
+// gfx950's transposing LDS read (ds_read_b64_tr_b16) delivers them: within a
+// 16-lane group, source lane s reads 4 columns of row (s / 4) and the hardware
+// hands lane i the 4 rows of column i, so one fragment is two such reads (rows
+// m .. m+3 and m+4 .. m+7).  The 16-byte chunks of a row are XOR-permuted and,
+// for 32-byte rows, the rows of a 16-row block too, so that the 8 rows x 32
+// bytes a half-wave reads land on distinct banks for every row width
+// (wg_sw / wg_slot).  Rows past the chunk are DMA'd from its last row (valid
+// memory) and zeroed in the fragments of the last step.
 // MFMA: v_mfma_f32_16x16x32_bf16 (ranks of 16 waste nothing).
 #include <type_traits>
 
@@ -81,51 +83,75 @@ __device__ __forceinline__ void wg_store(const WArgs &a, int e, int p, int q, fl
 
 typedef __attribute__((address_space(3))) void *wg_lds_ptr;
 
-// 16-byte chunk c of LDS row m (NCH chunks per row) sits at this physical chunk.
-template <int NCH>
-__device__ __forceinline__ int wg_chunk(int m, int c) {
-  return (c ^ (((m >> 3) & 3) << 1)) & (NCH - 1);
+typedef short wg_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) wg_v4i16 *wg_lds_v4;
+
+// LDS placement of a tile with NCH 16-byte chunks per row: row m sits in row
+// slot wg_slot(m) (a permutation within 16-row blocks, only for 32-byte rows)
+// and its chunk c at physical chunk c ^ wg_sw(m).  A transposing read of a
+// half-wave covers rows {8g + j, 8g + 8 + j : j < 4} (or j in 4..7) and two
+// adjacent chunks; the permutations give those 8 row pieces 8 distinct 32-byte
+// bank windows (and the 4 of one 16-lane group distinct 32-byte windows within
+// 128 bytes).  Both are involutions, so the DMA uses the same functions to find
+// the source row and chunk of an LDS position.
+template <int NCH> __device__ __forceinline__ int wg_slot(int m) {
+  return NCH == 2 ? m ^ (((m >> 3) & 1) << 2) : m;
+}
+template <int NCH> __device__ __forceinline__ int wg_sw(int m) {
+  if constexpr (NCH >= 16) return ((m & 3) | (((m >> 3) & 1) << 2)) << 1;
+  else if constexpr (NCH == 8) return ((m & 3) ^ ((m >> 3) & 1)) << 1;
+  else if constexpr (NCH == 4) return (((m >> 1) & 1) ^ ((m >> 3) & 1)) << 1;
+  else return 0;
+}
+template <int NCH> __device__ __forceinline__ int wg_off(int m, int col) {
+  return wg_slot<NCH>(m) * (NCH * 16) + ((((col >> 3) ^ wg_sw<NCH>(m)) & (NCH - 1)) << 4) +
+         ((col & 7) << 1);
 }
 
-// Byte offset of element (m, col) in a swizzled row-major LDS tile.
+// Lane byte offsets (first k-step) of the two transposing reads of the fragment
+// whose 16 columns start at colbase: rows 8*g4 + s/4 (+4), columns colbase +
+// 4*(s%4) .. +3, where s = lane % 16 and g4 = lane / 16.  Later k-steps of 32
+// rows add 32 rows' bytes (the permutations repeat every 16 rows).
 template <int NCH>
-__device__ __forceinline__ int wg_eoff(int m, int col) {
-  return m * (NCH * 16) + (wg_chunk<NCH>(m, col >> 3) << 4) + ((col & 7) << 1);
+__device__ __forceinline__ int2 wg_frag_offs(int g4, int s, int colbase) {
+  const int r = 8 * g4 + (s >> 2), col = colbase + 4 * (s & 3);
+  return make_int2(wg_off<NCH>(r, col), wg_off<NCH>(r + 4, col));
 }
 
-// Operand fragment of one 16x16x32 MFMA: 8 consecutive rows m0 + 8*(lane/16)
-// .. +7 of column col (lane%16 chosen by the caller), rows >= mlim as zero.
-template <int NCH, bool MASK>
-__device__ __forceinline__ bf16x8 wg_frag(const char *tile, int mb, int col, int mlim) {
-  uint32_t w[4];
+// Operand fragment of one 16x16x32 MFMA: rows mb .. mb+7 (mb = the lane group's
+// first row) of one column, rows >= mlim as zero.
+template <bool MASK>
+__device__ __forceinline__ bf16x8 wg_frag(const char *lo_p, const char *hi_p, int mb, int mlim) {
+  wg_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((wg_lds_v4)lo_p);
+  wg_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((wg_lds_v4)hi_p);
+  if (MASK) {
 #pragma unroll
-  for (int t = 0; t < 8; t += 2) {
-    uint32_t lo = *(const unsigned short *)(tile + wg_eoff<NCH>(mb + t, col));
-    uint32_t hi = *(const unsigned short *)(tile + wg_eoff<NCH>(mb + t + 1, col));
-    if (MASK) {
-      lo = mb + t < mlim ? lo : 0u;
-      hi = mb + t + 1 < mlim ? hi : 0u;
+    for (int j = 0; j < 4; ++j) {
+      lo[j] = mb + j < mlim ? lo[j] : (short)0;
+      hi[j] = mb + 4 + j < mlim ? hi[j] : (short)0;
     }
-    w[t >> 1] = lo | (hi << 16);
   }
   bf16x8 v;
-  __builtin_memcpy(&v, w, 16);
+  __builtin_memcpy(&v, &lo, 8);
+  __builtin_memcpy((char *)&v + 8, &hi, 8);
   return v;
 }
 
-// WP x WQ waves; each wave owns TP x TQ blocks of 16x16 outputs.
-template <int BQ, int WP, int WQ, int TP, int TQ>
-__global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
-  constexpr int kWgBP = wg_bp(BQ), NW = WP * WQ, kWgThreads = NW * 64;
+// WP x WQ compute waves, each owning TP x TQ blocks of 16x16 outputs, and NP
+// DMA waves that issue every global->LDS copy of the ring.
+template <int BQ, int WP, int WQ, int TP, int TQ, int NP>
+__global__ __launch_bounds__((WP * WQ + NP) * 64) void wgrad_kernel(const WArgs a) {
+  constexpr int kWgBP = wg_bp(BQ), NW = WP * WQ, kWgThreads = (NW + NP) * 64;
   static_assert(WP * TP * 16 == kWgBP && WQ * TQ * 16 == BQ, "tile");
   constexpr int NCL = kWgBP / 8, NCR = BQ / 8;  // 16-byte chunks per L / R row
   constexpr int L_BYTES = kWgBK * kWgBP * 2, R_BYTES = kWgBK * BQ * 2;
   constexpr int STAGE = L_BYTES + R_BYTES;
-  constexpr int LI = L_BYTES / 1024 / NW;                 // L DMA instructions per wave
-  constexpr int RI = R_BYTES >= 1024 * NW ? R_BYTES / 1024 / NW : 1;
-  constexpr int R_LANES = R_BYTES >= 1024 * NW ? 64 : R_BYTES / 16 / NW;  // active lanes
+  constexpr int LI = L_BYTES / 1024 / NP;                 // L DMA instructions per DMA wave
+  constexpr int RI = R_BYTES >= 1024 * NP ? R_BYTES / 1024 / NP : 1;
+  constexpr int R_LANES = R_BYTES >= 1024 * NP ? 64 : R_BYTES / 16 / NP;  // active lanes
   constexpr int G = LI + RI;                              // DMA instructions per stage
-  static_assert(LI >= 1 && R_LANES >= 1 && RI * R_LANES * 16 * NW == R_BYTES, "DMA split");
+  static_assert(LI >= 1 && R_LANES >= 1 && RI * R_LANES * 16 * NP == R_BYTES, "DMA split");
+  static_assert(G <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(16))) char lds[kWgStages * STAGE];
   __shared__ int32_t lrow_s[kWgChunkRows], rrow_s[kWgChunkRows];
 
@@ -151,7 +177,9 @@ __global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
   const int nrows = m1 - m0;  // >= 1
   const int p0 = ty * kWgBP, q0 = tz * BQ;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wp = wave % WP, wq = wave / WP;
+  const bool dma_wave = wave >= NW;   // wave-uniform role
+  const int dw = dma_wave ? wave - NW : 0;
+  const int wp = wave % WP, wq = (wave / WP) % WQ;
   const int l16 = lane & 15, g4 = lane >> 4;
 
   // the chunk's source rows, staged once
@@ -161,40 +189,80 @@ __global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
   }
   __syncthreads();
 
-  // DMA slots of this lane: L instruction i covers rows (wave*LI + i) * RPI_L +
-  // lane / NCL of a stage (RPI_L = 1024 / (NCL*16) rows per instruction);
-  // R instruction i covers bytes ((wave*RI + i) * R_LANES + lane) * 16.
-  const char *lbase = (const char *)a.l;
-  const char *rbase = (const char *)a.r;
-  auto issue = [&](int ks) __attribute__((always_inline)) {
-    char *st = lds + (ks % kWgStages) * STAGE;
-    const int mb = ks * kWgBK;
+  auto next_stage = [](int sb) { return sb + STAGE == kWgStages * STAGE ? 0 : sb + STAGE; };
+  const int nk = (nrows + kWgBK - 1) / kWgBK;
+
+  // One barrier per step, executed by both roles (their loops are separate so
+  // that each keeps only its own registers).  DMA waves: wait until stage ks
+  // has landed (stage ks+1 may still be in flight), barrier, then refill the
+  // slot of stage ks-1 (free: every compute wave has passed the barrier after
+  // computing it) with stage ks+kWgStages-1.  Compute waves: barrier, then
+  // compute stage ks while the DMA waves issue and wait.
+  if (dma_wave) {
+    // DMA slots of this lane, the same for every step: L instruction i of DMA
+    // wave dw writes stage bytes ((dw*LI + i) * 64 + lane) * 16, R instruction
+    // i the bytes ((dw*RI + i) * R_LANES + lane) * 16 after the L tile.  Such a
+    // position is (row slot, physical chunk pc); it receives row wg_slot(slot)
+    // of the step at logical chunk pc ^ wg_sw(row).  What does not depend on
+    // the step (the row within the step and the column bytes) is set here.
+    int l_rs[LI], r_rs[RI];
+    const char *l_src[LI], *r_src[RI];
 #pragma unroll
     for (int i = 0; i < LI; ++i) {
-      const int off = ((wave * LI + i) * 64 + lane) * 16;
-      const int rl = off / (NCL * 16), pc = (off / 16) % NCL;
-      int m = mb + rl;
-      m = m < nrows ? m : nrows - 1;
-      int col = p0 + ((pc ^ (((rl >> 3) & 3) << 1)) & (NCL - 1)) * 8;
+      const int off = ((dw * LI + i) * 64 + lane) * 16;
+      const int rs = wg_slot<NCL>(off / (NCL * 16)), pc = (off / 16) % NCL;
+      int col = p0 + ((pc ^ wg_sw<NCL>(rs)) & (NCL - 1)) * 8;
       col = col < a.P ? col : a.P - 8;
-      const char *g = lbase + ((int64_t)lrow_s[m] * a.ldl + col) * 2;
-      __builtin_amdgcn_global_load_lds(g, (wg_lds_ptr)(st + (wave * LI + i) * 1024), 16, 0, 0);
+      l_rs[i] = rs;
+      l_src[i] = (const char *)a.l + col * 2;
     }
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
-      if (lane < R_LANES) {
-        const int off = ((wave * RI + i) * R_LANES + lane) * 16;
-        const int rl = off / (NCR * 16), pc = (off / 16) % NCR;
-        int m = mb + rl;
-        m = m < nrows ? m : nrows - 1;
-        int col = q0 + ((pc ^ (((rl >> 3) & 3) << 1)) & (NCR - 1)) * 8;
-        col = col < a.Q ? col : a.Q - 8;
-        const char *g = rbase + ((int64_t)rrow_s[m] * a.ldr + col) * 2;
-        __builtin_amdgcn_global_load_lds(
-            g, (wg_lds_ptr)(st + L_BYTES + (wave * RI + i) * R_LANES * 16), 16, 0, 0);
+      const int off = ((dw * RI + i) * R_LANES + (lane < R_LANES ? lane : 0)) * 16;
+      const int rs = wg_slot<NCR>(off / (NCR * 16)), pc = (off / 16) % NCR;
+      int col = q0 + ((pc ^ wg_sw<NCR>(rs)) & (NCR - 1)) * 8;
+      col = col < a.Q ? col : a.Q - 8;
+      r_rs[i] = rs;
+      r_src[i] = (const char *)a.r + col * 2;
+    }
+    const uint32_t ldl2 = (uint32_t)a.ldl * 2u, ldr2 = (uint32_t)a.ldr * 2u;  // < 2^31 (host check)
+    auto issue = [&](int ks, int sb) __attribute__((always_inline)) {
+      char *st = lds + sb;
+      const int mb = ks * kWgBK;
+#pragma unroll
+      for (int i = 0; i < LI; ++i) {
+        const int m = min(mb + l_rs[i], nrows - 1);
+        const char *g = l_src[i] + (uint64_t)(uint32_t)lrow_s[m] * ldl2;
+        __builtin_amdgcn_global_load_lds(g, (wg_lds_ptr)(st + (dw * LI + i) * 1024), 16, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < RI; ++i) {
+        if (lane < R_LANES) {
+          const int m = min(mb + r_rs[i], nrows - 1);
+          const char *g = r_src[i] + (uint64_t)(uint32_t)rrow_s[m] * ldr2;
+          __builtin_amdgcn_global_load_lds(
+              g, (wg_lds_ptr)(st + L_BYTES + (dw * RI + i) * R_LANES * 16), 16, 0, 0);
+        }
+      }
+    };
+    int s_iss = 0;
+#pragma unroll
+    for (int s = 0; s < kWgStages - 1; ++s)
+      if (s < nk) {
+        issue(s, s_iss);
+        s_iss = next_stage(s_iss);
+      }
+    for (int ks = 0; ks < nk; ++ks) {
+      if (ks + 1 < nk) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(G) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (ks + kWgStages - 1 < nk) {
+        issue(ks + kWgStages - 1, s_iss);
+        s_iss = next_stage(s_iss);
       }
     }
-  };
+    return;
+  }
 
   f32x4 acc[TP][TQ];
 #pragma unroll
@@ -204,21 +272,33 @@ __global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][jj][v] = 0.0f;
 
-  auto compute = [&](int ks, auto mask_tag) __attribute__((always_inline)) {
+  int2 offl[TP], offr[TQ];
+#pragma unroll
+  for (int i = 0; i < TP; ++i) offl[i] = wg_frag_offs<NCL>(g4, l16, wp * TP * 16 + i * 16);
+#pragma unroll
+  for (int jj = 0; jj < TQ; ++jj) offr[jj] = wg_frag_offs<NCR>(g4, l16, wq * TQ * 16 + jj * 16);
+
+  // sb: byte offset of the step's stage (a scalar, so that every fragment
+  // address is one add plus immediate offsets)
+  auto compute = [&](int sb, int mlim, auto mask_tag) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
-    const char *tl = lds + (ks % kWgStages) * STAGE;
+    const char *tl = lds + sb;
     const char *tr = tl + L_BYTES;
-    const int mlim = nrows - ks * kWgBK;
 #pragma unroll
     for (int kk = 0; kk < kWgBK / 32; ++kk) {
       const int mb = kk * 32 + 8 * g4;
       bf16x8 af[TP], bq[TQ];
 #pragma unroll
-      for (int i = 0; i < TP; ++i)
-        af[i] = wg_frag<NCL, MASK>(tl, mb, wp * TP * 16 + i * 16 + l16, mlim);
+      for (int i = 0; i < TP; ++i) {
+        const char *lp = tl + offl[i].x + kk * 32 * (NCL * 16);
+        af[i] = wg_frag<MASK>(lp, lp + 4 * (NCL * 16), mb, mlim);
+      }
 #pragma unroll
-      for (int jj = 0; jj < TQ; ++jj)
-        bq[jj] = wg_frag<NCR, MASK>(tr, mb, wq * TQ * 16 + jj * 16 + l16, mlim);
+      for (int jj = 0; jj < TQ; ++jj) {
+        const char *rp = tr + offr[jj].x + kk * 32 * (NCR * 16);
+        const char *rh = NCR == 2 ? tr + offr[jj].y + kk * 32 * (NCR * 16) : rp + 4 * (NCR * 16);
+        bq[jj] = wg_frag<MASK>(rp, rh, mb, mlim);
+      }
 #pragma unroll
       for (int i = 0; i < TP; ++i)
 #pragma unroll
@@ -227,23 +307,15 @@ __global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
     }
   };
 
-  const int nk = (nrows + kWgBK - 1) / kWgBK;
-#pragma unroll
-  for (int s = 0; s < kWgStages - 1; ++s)
-    if (s < nk) issue(s);
-  for (int ks = 0; ks < nk; ++ks) {
-    // stage ks landed (at most kWgStages-2 later stages in flight), then the
-    // slot of stage ks-1 is free for stage ks+kWgStages-1
-    const int pend = (nk - 1 - ks) < (kWgStages - 2) ? (nk - 1 - ks) : (kWgStages - 2);
-    if (pend >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(G) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  int s_comp = 0;
+  for (int ks = 0; ks < nk - 1; ++ks) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (ks + kWgStages - 1 < nk) issue(ks + kWgStages - 1);
-    if (ks == nk - 1 && (nrows & (kWgBK - 1)))
-      compute(ks, std::true_type{});
-    else
-      compute(ks, std::false_type{});
+    compute(__builtin_amdgcn_readfirstlane(s_comp), kWgBK, std::false_type{});
+    s_comp = next_stage(s_comp);
   }
+  // last step: rows past the chunk masked
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  compute(__builtin_amdgcn_readfirstlane(s_comp), nrows - (nk - 1) * kWgBK, std::true_type{});
 
   // Accumulator element v of a 16x16 block: row 4*(lane/16) + v, column lane%16.
   // (a multi-chunk expert without workspace means M understated the rows:
@@ -268,35 +340,45 @@ __global__ __launch_bounds__(WP *WQ * 64) void wgrad_kernel(const WArgs a) {
 }
 
 // Outputs of the experts without exactly one chunk: their chunk partials
-// summed in chunk order (no chunk: zero).  One workgroup per (expert, tile).
+// summed in chunk order (no chunk: zero).  A thread owns 4 consecutive
+// elements of one tile row (float4 loads of every chunk's partial); blockIdx.y
+// is the expert, blockIdx.x the (tile, 1024-element piece).
+constexpr int kWgRedThreads = 256;
 template <int BQ>
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const WArgs a) {
-  constexpr int kWgBP = wg_bp(BQ);
-  const int e = blockIdx.x;
+__global__ __launch_bounds__(kWgRedThreads) void wgrad_reduce_kernel(const WArgs a) {
+  constexpr int kWgBP = wg_bp(BQ), PIECES = kWgBP * BQ / (4 * kWgRedThreads);
+  static_assert(PIECES * 4 * kWgRedThreads == kWgBP * BQ, "reduce split");
+  const int e = blockIdx.y;
   const int32_t *cpre = a.seg + kWgChunkSegRow * (a.E + 1);
   const int c0 = cpre[e], nce = cpre[e + 1] - c0;
   if (nce == 1 || (nce == 0 && a.mode == ART_MOE_WGRAD_ACCUMULATE)) return;
   if (nce > 1 && a.ws == nullptr) return;
-  const int p0 = blockIdx.y * kWgBP, q0 = blockIdx.z * BQ;
-  for (int t = threadIdx.x; t < kWgBP * BQ; t += 256) {
-    const int pl = t / BQ, ql = t - pl * BQ;
-    if (p0 + pl >= a.P || q0 + ql >= a.Q) continue;
-    // partials of 8 chunks are loaded before they are added (same chunk order
-    // as a plain loop: the sum is identical, the loads overlap)
+  const int tile = blockIdx.x / PIECES, piece = blockIdx.x - tile * PIECES;
+  const int ty = tile % a.n_pt, tz = tile / a.n_pt;
+  const int t = (piece * kWgRedThreads + threadIdx.x) * 4;  // element in the tile
+  const int pl = t / BQ, ql = t - pl * BQ;
+  const int p = ty * kWgBP + pl, q = tz * BQ + ql;
+  if (p >= a.P || q >= a.Q) return;
+  f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (nce > 1) {
+    // partials of 8 chunks are loaded before they are added (same chunk
+    // order as a plain loop: the sum is identical, the loads overlap)
     const size_t cstride = (size_t)a.n_pt * a.n_qt * (kWgBP * BQ);
-    const float *src = a.ws + (((size_t)c0 * a.n_pt + blockIdx.y) * a.n_qt + blockIdx.z) *
-                                  (size_t)(kWgBP * BQ) + t;
-    float s = 0.0f;
+    const float *src = a.ws + (((size_t)c0 * a.n_pt + ty) * a.n_qt + tz) * (size_t)(kWgBP * BQ) + t;
     for (int cb = 0; cb < nce; cb += 8) {
-      float v[8];
+      f32x4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = cb + u < nce ? src[(size_t)(cb + u) * cstride] : 0.0f;
+      for (int u = 0; u < 8; ++u)
+        v[u] = cb + u < nce ? *(const f32x4 *)(src + (size_t)(cb + u) * cstride)
+                            : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int u = 0; u < 8; ++u)
         if (cb + u < nce) s += v[u];
     }
-    wg_store(a, e, p0 + pl, q0 + ql, s);
   }
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    if (q + v < a.Q) wg_store(a, e, p, q + v, s[v]);
 }
 
 static int wgrad_bq(int Q) { return Q <= 16 ? 16 : Q <= 32 ? 32 : Q <= 64 ? 64 : 128; }
@@ -305,7 +387,7 @@ static int64_t wgrad_max_chunks(int64_t M, int E) {
   return (M + kWgChunkRows - 1) / kWgChunkRows + E;
 }
 
-template <int BQ, int WP, int WQ, int TP, int TQ>
+template <int BQ, int WP, int WQ, int TP, int TQ, int NP>
 static int launch_wgrad(WArgs a, int64_t M, hipStream_t s) {
   a.n_pt = (a.P + wg_bp(BQ) - 1) / wg_bp(BQ);
   a.n_qt = (a.Q + BQ - 1) / BQ;
@@ -313,10 +395,12 @@ static int launch_wgrad(WArgs a, int64_t M, hipStream_t s) {
     const int64_t groups = (wgrad_max_chunks(M, a.E) + 7) / 8;  // chunk groups of 8 (one per XCD)
     const int64_t blocks = groups * 8 * a.n_pt * a.n_qt;
     ART_REQUIRE(blocks < (int64_t)1 << 31, "grouped_wgrad: too many tiles");
-    wgrad_kernel<BQ, WP, WQ, TP, TQ><<<dim3((unsigned)blocks), WP * WQ * 64, 0, s>>>(a);
+    wgrad_kernel<BQ, WP, WQ, TP, TQ, NP><<<dim3((unsigned)blocks), (WP * WQ + NP) * 64, 0, s>>>(a);
     if (int rc = check_launch("grouped_wgrad")) return rc;
   }
-  wgrad_reduce_kernel<BQ><<<dim3((unsigned)a.E, a.n_pt, a.n_qt), 256, 0, s>>>(a);
+  constexpr int pieces = wg_bp(BQ) * BQ / (4 * kWgRedThreads);
+  wgrad_reduce_kernel<BQ><<<dim3((unsigned)(a.n_pt * a.n_qt * pieces), (unsigned)a.E), kWgRedThreads,
+                            0, s>>>(a);
   return check_launch("grouped_wgrad reduce");
 }
 
@@ -344,6 +428,8 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   ART_REQUIRE(P > 0 && Q > 0 && P % 8 == 0 && Q % 8 == 0,
               "grouped_wgrad: P and Q must be positive multiples of 8 (P=%d Q=%d)", P, Q);
   ART_REQUIRE(ldl % 8 == 0 && ldr % 8 == 0, "grouped_wgrad: row strides must be multiples of 8");
+  ART_REQUIRE(ldl < ((int64_t)1 << 30) && ldr < ((int64_t)1 << 30),
+              "grouped_wgrad: row strides must be below 2^30 elements");
   ART_REQUIRE(lm && r && seg && out, "grouped_wgrad: null pointer");
   ART_REQUIRE(((uintptr_t)lm & 15) == 0 && ((uintptr_t)r & 15) == 0,
               "grouped_wgrad: operands must be 16-byte aligned");
@@ -356,6 +442,7 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   ART_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "grouped_wgrad: needs a workspace of %zu bytes (art_moe_wgrad_workspace_bytes)",
               need);
+  ART_REQUIRE(((uintptr_t)workspace & 15) == 0, "grouped_wgrad: workspace must be 16-byte aligned");
   WArgs a{};
   a.l = (const bf16 *)lm; a.ldl = ldl; a.l_rows = l_rows;
   a.r = (const bf16 *)r; a.ldr = ldr; a.r_rows = r_rows;
@@ -366,9 +453,9 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   a.ws = (float *)workspace;
   hipStream_t s = as_stream(stream);
   switch (wgrad_bq(Q)) {
-    case 16: return launch_wgrad<16, 4, 1, 2, 1>(a, M, s);
-    case 32: return launch_wgrad<32, 4, 1, 2, 2>(a, M, s);
-    case 64: return launch_wgrad<64, 4, 2, 4, 2>(a, M, s);
-    default: return launch_wgrad<128, 4, 2, 4, 4>(a, M, s);
+    case 16: return launch_wgrad<16, 4, 1, 2, 1, 2>(a, M, s);
+    case 32: return launch_wgrad<32, 4, 1, 2, 2, 2>(a, M, s);
+    case 64: return launch_wgrad<64, 4, 2, 4, 2, 2>(a, M, s);
+    default: return launch_wgrad<128, 4, 2, 4, 4, 2>(a, M, s);
   }
 }

@@ -241,7 +241,8 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
  *   out[e*o_es + p*o_ps + q*o_qs] (+)=
  *       alpha * sum_{m in segment e} Lm[lrow(m), p] * R[rrow(m), q]
  * Lm bf16 rows (ldl) with lrow(m) = l_rows ? l_rows[m] : m, likewise R;
- * P, Q, ldl, ldr multiples of 8, operands 16-byte aligned.
+ * P, Q, ldl, ldr multiples of 8 (ldl, ldr < 2^30), operands and workspace
+ * 16-byte aligned.
  * (o_ps, o_qs) = (Q, 1) writes [E][P][Q], (1, P) writes the transpose
  * [E][Q][P].  mode: ART_MOE_WGRAD_STORE writes fp32 out, _ACCUMULATE adds to
  * fp32 out, _STORE_BF16 writes bf16 out (one rounding of the fp32 sum: the

@@ -157,7 +157,8 @@ def test_fc2_dgrad_swiglu(device, e, m, f, h, kt):
 @pytest.mark.parametrize("e,m,p,q,gather,transpose", [
     (8, 1000, 256, 16, True, False), (128, 4096, 2048, 32, False, False),
     (16, 2000, 768, 16, False, True), (4, 300, 64, 128, True, True), (6, 500, 96, 48, False, False),
-    (5, 21000, 264, 72, True, False), (3, 9000, 128, 128, False, True)])
+    (5, 21000, 264, 72, True, False), (3, 9000, 128, 128, False, True),
+    (4, 700, 8, 8, True, False), (2, 5000, 40, 24, False, True), (7, 3000, 520, 64, True, False)])
 def test_grouped_wgrad(device, e, m, p, q, gather, transpose):
     ops = _ops()
     print(f"wgrad e={e} m={m} p={p} q={q}", flush=True)
