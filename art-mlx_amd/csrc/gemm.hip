@@ -510,6 +510,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     barrier_nofence();                                                                        \
     if ((ks) + STAGES - 1 < nk) ART_ISSUE((ks) + STAGES - 1);                                 \
   } while (0)
+    // Staggered issue in the full k-tiles of 256-row tiles: waves 0..NW/2-1
+    // issue their share of the next stage right after the barrier, the other
+    // half (the second wave on each SIMD) halfway through its MFMAs of the
+    // stage, so one wave per SIMD keeps the matrix core busy while the other
+    // waits on the address unit.  The slot being filled was released by the
+    // barrier either way, and each wave still issues its stages in order.
+    const bool late_issue = BM == 256 && wave >= NW / 2;
+#define ART_STAGE_IN_STAGGERED(ks)                                                            \
+  do {                                                                                        \
+    const int pend_ = (nk - 1 - (ks)) < (STAGES - 2) ? (nk - 1 - (ks)) : (STAGES - 2);        \
+    wait_stages<G, STAGES - 2>(pend_);                                                        \
+    barrier_nofence();                                                                        \
+    if (!late_issue && (ks) + STAGES - 1 < nk) ART_ISSUE((ks) + STAGES - 1);                  \
+  } while (0)
 
     // Full k-tiles of the base product: branch-free, fragments of step kk+1
     // are read while step kk multiplies.  (A separate loop keeps the
@@ -540,16 +554,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         __builtin_amdgcn_sched_barrier(0);
         mma_step<TM, TN>(acc, af0, bf0);
         __builtin_amdgcn_sched_barrier(0);
-        if (ks + 1 < nk) ART_STAGE_IN(ks + 1);
+        if (ks + 1 < nk) ART_STAGE_IN_STAGGERED(ks + 1);
         if (ks + 1 < nk_full)
           load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem + ((ks + 1) % STAGES) * STAGE_BYTES, 0,
                                                     wm, wn, lrow, lk, af0, bf0);
         __builtin_amdgcn_sched_barrier(0);
         mma_step<TM, TN>(acc, af1, bf1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (late_issue && ks + STAGES < nk) ART_ISSUE(ks + STAGES);
       }
     } else {
     for (int ks = 0; ks < nk_full; ++ks) {
-      ART_STAGE_IN(ks);
+      ART_STAGE_IN_STAGGERED(ks);
       const char *st = smem + (ks % STAGES) * STAGE_BYTES;
       bf16x8 af0[TM], bf0[TN], af1[TM], bf1[TN];
       // Fragment reads of step kk+1 are issued before the MFMAs of step kk;
@@ -568,6 +584,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         ART_FENCE();
         mma_step<TM, TN>(acc, af1, bf1);
         ART_FENCE();
+        if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
+        ART_FENCE();
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 3, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
       } else {
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
@@ -578,6 +596,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
         ART_FENCE();
         mma_step<TM, TN>(acc, af1, bf1);
+        ART_FENCE();
+        if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
         ART_FENCE();
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
       }
@@ -610,6 +630,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       }
     }
 #undef ART_STAGE_IN
+#undef ART_STAGE_IN_STAGGERED
 #undef ART_ISSUE
 #undef ART_ISSUE_LORA
     barrier_nofence();  // every wave is done reading the ring: reuse it for staging
