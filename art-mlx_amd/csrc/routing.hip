@@ -364,73 +364,151 @@ __global__ __launch_bounds__(256) void combine_kernel(
 }
 
 // ---------------------------------------------------------- router LoRA
-// One wavefront per 4 tokens, lanes over the E logit columns; t_r rows are
-// wave-uniform reads, B rows coalesced and L1/L2-resident (r*E*2 bytes).
+// logits[t, :] += scale * t_r[t, :] B over 64-token tiles.  LDS holds the
+// tile's t_r transposed, [rank][token] with a 68-float row (16-byte aligned,
+// and the transposing writes spread over 16 banks), and one 64-column chunk of
+// B as fp32 [rank][64]: dynamic size (68 + 64) * rp floats, rp = the rank
+// padded to 4.  Wave w owns tokens 16w .. 16w+15 of the tile and lane l column
+// l of the chunk; per rank step it reads its 16 tokens' t_r values as four
+// broadcast float4s and one B value, four rank steps' reads issued together.
+constexpr int kLoraTileTokens = 64, kLoraCols = 64, kLoraMaxRank = 256, kLoraTrRow = 68;
+
 __global__ __launch_bounds__(256) void router_lora_apply_kernel(
     const float *__restrict__ t_r, int64_t T, int r, const bf16 *__restrict__ b, int E,
     float scale, float *__restrict__ logits, bf16 *__restrict__ t_bf16) {
-  const int lane = lane_id();
-  const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
-  if (t0 >= T) return;
-  const int nt = (int)(T - t0 < 4 ? T - t0 : 4);
-  const float *tr = t_r + t0 * r;
-  for (int e = lane; e < E; e += kWave) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = 0; i < r; ++i) {
-      const float bv = (float)b[(int64_t)i * E + e];
+  extern __shared__ __attribute__((aligned(16))) float lora_s[];
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kLoraTileTokens;
+  const int nt = (int)(T - t0 < kLoraTileTokens ? T - t0 : kLoraTileTokens);
+  const int rp = (r + 3) & ~3;  // rank padded to 4 (zeros)
+  float *tr_s = lora_s, *b_s = lora_s + kLoraTrRow * rp;
+  for (int i = lane; i < rp; i += kWave) {  // lanes along the rank, 16 token rows per wave
+    float v[16];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (u < nt) acc[u] += tr[u * r + i] * bv;
+    for (int q = 0; q < 16; ++q) {  // loads first, so all 16 are in flight together
+      const int u = wave + 4 * q;
+      v[q] = (u < nt && i < r) ? t_r[(t0 + u) * r + i] : 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (u < nt) logits[(t0 + u) * E + e] += scale * acc[u];
+    for (int q = 0; q < 16; ++q) {
+      const int u = wave + 4 * q;
+      tr_s[i * kLoraTrRow + u] = v[q];
+      if (t_bf16 && u < nt && i < r) t_bf16[(t0 + u) * r + i] = (bf16)v[q];
+    }
   }
-  if (t_bf16)
-    for (int p = lane; p < nt * r; p += kWave) t_bf16[t0 * r + p] = (bf16)tr[p];
+  const float *trw = tr_s + wave * 16;
+  for (int e0 = 0; e0 < E; e0 += kLoraCols) {
+    __syncthreads();  // tr_s written / the previous chunk of b_s consumed
+    for (int i0 = wave; i0 < rp; i0 += 4 * 8) {  // rank rows, lanes along the columns
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = i0 + 4 * q;
+        v[q] = (i < r && e0 + lane < E) ? (float)b[(int64_t)i * E + e0 + lane] : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (i0 + 4 * q < rp) b_s[(i0 + 4 * q) * kLoraCols + lane] = v[q];
+    }
+    __syncthreads();
+    float acc[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) acc[u] = 0.0f;
+    for (int i = 0; i < rp; i += 4) {
+      float bv[4];
+      float4 tv[4][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        bv[c] = b_s[(i + c) * kLoraCols + lane];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) tv[c][q] = *(const float4 *)(trw + (i + c) * kLoraTrRow + 4 * q);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[4 * q + 0] += tv[c][q].x * bv[c];
+          acc[4 * q + 1] += tv[c][q].y * bv[c];
+          acc[4 * q + 2] += tv[c][q].z * bv[c];
+          acc[4 * q + 3] += tv[c][q].w * bv[c];
+        }
+    }
+    const int e = e0 + lane;
+    if (e < E) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int tu = wave * 16 + u;
+        if (tu < nt) logits[(t0 + tu) * E + e] += scale * acc[u];
+      }
+    }
+  }
 }
 
-// B^T staged in LDS ([E][r] bf16) once per block; each wavefront then walks
-// its tokens: lane i of g sums the k selected columns of B, and the dense
-// bf16 dlogits row is written with lanes over E.
-constexpr int kLoraGradTokens = 64;  // tokens per workgroup
+// B^T staged in LDS ([E][r] bf16) once per block; each wavefront walks its
+// tokens in batches of 64 / k, whose ids and weights one load brings in (lane
+// l holds slot l % k of the batch's token l / k): lane i of g sums the k
+// selected columns of B, and the dense bf16 dlogits row is written with lanes
+// over E.
+constexpr int kLoraGradTokens = 64;  // tokens per workgroup (16 per wavefront)
 
 __global__ __launch_bounds__(256) void router_lora_grad_kernel(
     const float *__restrict__ dl, const int32_t *__restrict__ idx, int64_t T, int k,
     const bf16 *__restrict__ b, int r, int E, float scale, bf16 *__restrict__ g,
     bf16 *__restrict__ dlog) {
-  extern __shared__ bf16 bt[];
-  for (int p = threadIdx.x; p < r * E; p += blockDim.x) {
-    const int i = p / E, e = p - i * E;
-    bt[e * r + i] = b[p];
-  }
-  __syncthreads();
+  extern __shared__ bf16 bt[];  // [E][r + 2]: the padded row spreads the transposing writes
+  const int rs = r + 2;
   const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int64_t tb = (int64_t)blockIdx.x * kLoraGradTokens;
-  const int64_t te = tb + kLoraGradTokens < T ? tb + kLoraGradTokens : T;
-  for (int64_t t = tb + wave; t < te; t += 4) {
-    const bool act = lane < k;
-    const int my_e = act ? idx[t * k + lane] : -1;
-    const float my_dl = act ? dl[t * k + lane] : 0.0f;
-    for (int i0 = 0; i0 < r; i0 += kWave) {
-      const int i = i0 + lane;
-      float acc = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        const int e = __shfl(my_e, j, kWave);
-        const float lj = __shfl(my_dl, j, kWave);
-        if (e >= 0 && i < r) acc += lj * (float)bt[e * r + i];
+  for (int e = lane; e < E; e += kWave)
+    for (int i0 = wave; i0 < r; i0 += 4 * 8) {  // 8 loads in flight per lane
+      bf16 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = i0 + 4 * q;
+        v[q] = i < r ? b[(int64_t)i * E + e] : (bf16)0.0f;
       }
-      if (i < r) g[t * r + i] = (bf16)(scale * acc);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (i0 + 4 * q < r) bt[e * rs + i0 + 4 * q] = v[q];
     }
-    for (int e0 = 0; e0 < E; e0 += kWave) {
-      const int e = e0 + lane;
-      float v = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        const int ej = __shfl(my_e, j, kWave);
-        const float lj = __shfl(my_dl, j, kWave);
-        if (ej == e) v += lj;
+  __syncthreads();
+  const int64_t tb = (int64_t)blockIdx.x * kLoraGradTokens + wave * (kLoraGradTokens / 4);
+  const int64_t te = tb + kLoraGradTokens / 4 < T ? tb + kLoraGradTokens / 4 : T;
+  const int per = kWave / k;  // tokens per batch (k <= 32: at least 2)
+  for (int64_t t0 = tb; t0 < te; t0 += per) {
+    const int nb = (int)(te - t0 < per ? te - t0 : per);
+    const bool act = lane < nb * k;
+    const int my_e = act ? idx[t0 * k + lane] : -1;
+    const float my_dl = act ? dl[t0 * k + lane] : 0.0f;
+    for (int u = 0; u < nb; ++u) {
+      const int64_t t = t0 + u;
+      for (int i0 = 0; i0 < r; i0 += kWave) {
+        const int i = i0 + lane;
+        const int ic = i < r ? i : r - 1;
+        float acc = 0.0f;
+        for (int j0 = 0; j0 < k; j0 += 8) {  // 8 slots' LDS reads in flight together
+          float lj[8], bv[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int j = j0 + q < k ? j0 + q : k - 1;
+            const int e = __shfl(my_e, u * k + j, kWave);
+            lj[q] = (j0 + q < k && e >= 0) ? __shfl(my_dl, u * k + j, kWave) : 0.0f;
+            bv[q] = (float)bt[(e >= 0 ? e : 0) * rs + ic];
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc += lj[q] * bv[q];
+        }
+        if (i < r) g[t * r + i] = (bf16)(scale * acc);
       }
-      if (e < E) dlog[t * E + e] = (bf16)v;
+      for (int e0 = 0; e0 < E; e0 += kWave) {
+        const int e = e0 + lane;
+        float v = 0.0f;
+        for (int j = 0; j < k; ++j) {
+          const int ej = __shfl(my_e, u * k + j, kWave);
+          const float lj = __shfl(my_dl, u * k + j, kWave);
+          if (ej == e) v += lj;
+        }
+        if (e < E) dlog[t * E + e] = (bf16)v;
+      }
     }
   }
 }
@@ -735,9 +813,11 @@ extern "C" int art_moe_router_lora_apply(const float *t_r, int64_t T, int32_t r,
   ART_REQUIRE(T >= 0 && r >= 1 && E >= 1, "router_lora_apply: need T >= 0, r >= 1, E >= 1");
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(t_r && b && logits, "router_lora_apply: null pointer");
-  const int64_t waves = (T + 3) / 4;
-  router_lora_apply_kernel<<<dim3((unsigned)((waves + 3) / 4)), 256, 0, as_stream(stream)>>>(
-      t_r, T, r, (const bf16 *)b, E, scale, logits, (bf16 *)t_bf16);
+  ART_REQUIRE(r <= kLoraMaxRank, "router_lora_apply: rank must be <= %d (r=%d)", kLoraMaxRank, r);
+  const size_t lds = (size_t)(kLoraTrRow + kLoraCols) * ((r + 3) & ~3) * sizeof(float);
+  router_lora_apply_kernel<<<dim3((unsigned)((T + kLoraTileTokens - 1) / kLoraTileTokens)), 256, lds,
+                             as_stream(stream)>>>(t_r, T, r, (const bf16 *)b, E, scale, logits,
+                                                  (bf16 *)t_bf16);
   return check_launch("router_lora_apply");
 }
 
@@ -747,10 +827,11 @@ extern "C" int art_moe_router_lora_grad(const float *dl, const int32_t *idx, int
   clear_error();
   ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && r >= 1 && E >= 1,
               "router_lora_grad: need 1 <= k <= 32, r >= 1, E >= 1 (k=%d r=%d E=%d)", k, r, E);
-  ART_REQUIRE((int64_t)r * E <= 32768, "router_lora_grad: r * E must be <= 32768 (r=%d E=%d)", r, E);
+  ART_REQUIRE((int64_t)(r + 2) * E <= 65536,
+              "router_lora_grad: (r + 2) * E must be <= 65536 (r=%d E=%d)", r, E);
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(dl && idx && b && g && dlog, "router_lora_grad: null pointer");
-  const size_t lds = (size_t)r * E * sizeof(bf16);
+  const size_t lds = (size_t)(r + 2) * E * sizeof(bf16);
   router_lora_grad_kernel<<<dim3((unsigned)((T + kLoraGradTokens - 1) / kLoraGradTokens)), 256, lds,
                             as_stream(stream)>>>(dl, idx, T, k, (const bf16 *)b, r, E, scale,
                                                  (bf16 *)g, (bf16 *)dlog);

@@ -297,9 +297,9 @@ int art_moe_weighted_swiglu_back(const void *dh, const void *y1, const float *pr
  * (src/art/megatron/provider.py:605). */
 
 /* logits[t*E + e] += scale * sum_i t_r[t*r + i] * b[i*E + e]   (fp32)
- * t_r fp32 [T, r] = x A_r from an fp32-output product; b bf16 [r, E].
- * t_bf16 (optional) [T, r] receives t_r rounded to bf16 (operand of the
- * B_r gradient). */
+ * t_r fp32 [T, r] = x A_r from an fp32-output product; b bf16 [r, E];
+ * r <= 256.  t_bf16 (optional) [T, r] receives t_r rounded to bf16 (operand
+ * of the B_r gradient). */
 int art_moe_router_lora_apply(const float *t_r, int64_t T, int32_t r,
                               const void *b, int32_t E, float scale,
                               float *logits, void *t_bf16, void *stream);
@@ -310,7 +310,7 @@ int art_moe_router_lora_apply(const float *t_r, int64_t T, int32_t r,
  *                   (dx += g A_r^T, dA_r = x^T g)
  *   dlog[t*E + e] = bf16(sum_{j: idx[t,j] = e} dl[t,j])
  *                   (dense dlogits, dB_r = scale * t_r^T dlog)
- * r * E <= 32768. */
+ * (r + 2) * E <= 65536. */
 int art_moe_router_lora_grad(const float *dl, const int32_t *idx, int64_t T,
                              int32_t k, const void *b, int32_t r, int32_t E,
                              float scale, void *g, void *dlog, void *stream);

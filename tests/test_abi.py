@@ -87,7 +87,7 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert lib.art_moe_wgrad_workspace_bytes(2048, 128, 2048, 32) == 0
     assert lib.art_moe_wgrad_workspace_bytes(65536, 128, 2048, 32) == (32 + 128) * 2048 * 32 * 4
     rc = lib.art_moe_router_lora_grad(null, null, 8, 8, null, 512, 128, 1.0, null, null, null)
-    assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"r * E" in lib.art_moe_last_error()
+    assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"(r + 2) * E" in lib.art_moe_last_error()
 
 
 def test_python_call_raises_valueerror(lib):

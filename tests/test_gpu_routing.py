@@ -196,3 +196,43 @@ def test_combine_router_grad_addend_and_dropped_slots(device, k):
         ref += ok * wgt[:, j:j + 1].double() * yp[d.clamp_min(0)].double()
         ref += dl[:, j:j + 1].double() * w_r[idx[:, j].long()].double()
     torch.testing.assert_close(y.cpu().double(), ref, rtol=2 ** -7, atol=1e-5)
+
+
+@pytest.mark.parametrize("t,r,e", [(1000, 64, 128), (65, 5, 8), (64, 1, 100), (1, 16, 200),
+                                   (300, 256, 64)])
+def test_router_lora_apply_matches_fp32(device, t, r, e):
+    """logits += s * t_r B (fp32) over ragged token tiles, ranks not a multiple
+    of 4 and column counts not a multiple of 64; t_bf16 is t_r rounded once."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(t + r + e)
+    t_r = torch.randn(t, r, generator=g)
+    b = (torch.randn(r, e, generator=g) * 0.1).to(torch.bfloat16)
+    logits = torch.randn(t, e, generator=g)
+    out = logits.to(device)
+    t_bf = ops.router_lora_apply(t_r.to(device), b.to(device), out, 0.75, want_bf16=True)
+    ref = logits.double() + 0.75 * t_r.double() @ b.double()
+    torch.testing.assert_close(out.cpu().double(), ref, rtol=1e-5, atol=1e-5)
+    assert torch.equal(t_bf.cpu(), t_r.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("t,k,r,e", [(1000, 8, 64, 128), (77, 3, 5, 40), (1, 32, 16, 64),
+                                     (130, 20, 100, 300)])
+def test_router_lora_grad_matches_fp32(device, t, k, r, e):
+    """g = s * dl . B[:, idx] per token and the dense dlogits scatter, with some
+    slots dropped (idx = -1), k up to 32 (batches of 64 / k tokens per load)."""
+    ops = _ops()
+    g0 = torch.Generator().manual_seed(t + k + r)
+    idx = torch.stack([torch.randperm(e, generator=g0)[:k] for _ in range(t)]).to(torch.int32)
+    idx[torch.rand(t, k, generator=g0) < 0.1] = -1
+    dl = torch.randn(t, k, generator=g0)
+    b = (torch.randn(r, e, generator=g0) * 0.1).to(torch.bfloat16)
+    g, dlog = ops.router_lora_grad(dl.to(device), idx.to(device), b.to(device), 0.5)
+    ok = (idx >= 0).double()
+    cols = b.double()[:, idx.clamp_min(0).long()]            # [r, t, k]
+    g_ref = 0.5 * (cols * (dl.double() * ok).unsqueeze(0)).sum(-1).t()
+    dlog_ref = torch.zeros(t, e, dtype=torch.float64)
+    for j in range(k):
+        sel = idx[:, j] >= 0
+        dlog_ref[sel, idx[sel, j].long()] += dl[sel, j].double()
+    torch.testing.assert_close(g.cpu().double(), g_ref, rtol=2 ** -7, atol=1e-4)
+    torch.testing.assert_close(dlog.cpu().double(), dlog_ref, rtol=2 ** -7, atol=1e-4)
