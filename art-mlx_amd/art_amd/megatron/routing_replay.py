@@ -518,6 +518,33 @@ def build_moe_routing_replay_bundle_from_packed_tensors(
                                   num_steps=n_steps, max_topk=topk, router_keys=keys, steps=steps)
 
 
+# ---------------------------------------------- device-resident replay target
+class DeviceReplayTarget:
+    """A replay target kept as a device route table and a row map: token t
+    replays ``table[rows[t]]`` (table int32 [N, k], rows int32 [T], both on
+    the device).  The router kernels read it directly
+    (``ops.router_replay_rows``), so a step's table is uploaded once and a
+    micro's row map once for every router, instead of one host-gathered
+    [T, k] target per router call (routing_replay.py:1437-1474, 1530-1572)."""
+
+    def __init__(self, table: torch.Tensor, rows: torch.Tensor) -> None:
+        if table.dim() != 2 or rows.dim() != 1:
+            raise RuntimeError("DeviceReplayTarget needs table [N, k] and rows [T]")
+        self.table, self.rows = table, rows
+
+    @property
+    def shape(self) -> torch.Size:
+        return torch.Size((int(self.rows.shape[0]), int(self.table.shape[1])))
+
+    @property
+    def device(self) -> torch.device:
+        return self.table.device
+
+    def materialize(self) -> torch.Tensor:
+        """The [T, k] int64 target (for consumers that need the ids themselves)."""
+        return self.table.index_select(0, self.rows.long()).long()
+
+
 # ----------------------------------------------------- router replay object
 class RouterReplayAction(enum.Enum):
     RECORD = "record"
@@ -588,6 +615,8 @@ class RouterReplay:
         else the default top-k (recorded under RECORD)."""
         target = self.active_target()
         if target is not None:
+            if isinstance(target, DeviceReplayTarget):
+                target = target.materialize()
             ids = target.to(device=scores.device, dtype=torch.long)
             return scores.gather(1, ids), ids
         vals, ids = default_compute_topk(scores, topk, num_groups, group_topk)
@@ -678,7 +707,9 @@ class MoeRoutingReplayController:
 
     Life cycle per step: ``set_step`` -> for each micro ``begin_micro`` ->
     ``set_local_input_token_uids`` / ``prepare_micro_targets`` (targets are
-    built on the host and staged to the device on a side stream) -> the
+    built on the host and staged to the device on a side stream, or, with
+    ``device_targets``, kept as the step's device route table plus the
+    micro's device row map) -> the
     router's ``routing`` call installs the target -> ``finalize_step`` checks
     every expected call was consumed.  A second routing call for the same
     micro (activation recompute) reuses the previous call's route.
@@ -687,10 +718,13 @@ class MoeRoutingReplayController:
     def __init__(self, *, bundle: MoeRoutingReplayBundle, strict: bool,
                  local_token_indexer: Any | None = None, allow_recompute_reuse: bool = True,
                  device: torch.device | str | None = None,
-                 parallel_state: Any | None = None) -> None:
+                 parallel_state: Any | None = None, device_targets: bool = False) -> None:
         self.bundle = bundle
         self.strict = strict
         self.allow_recompute_reuse = allow_recompute_reuse
+        # device path: route tables uploaded once per step and row maps once
+        # per micro; routers replay table[rows[t]] (DeviceReplayTarget)
+        self.device_targets = device_targets
         self.parallel_state = parallel_state or SingleProcessParallelState()
         self.local_token_indexer = local_token_indexer or TopologyAwareLocalTokenIndexer(
             self.parallel_state)
@@ -710,6 +744,10 @@ class MoeRoutingReplayController:
         self._uid_dense_start: int | None = None
         self._uid_count = 0
         self._uid_rows: dict[int, int] = {}
+        if getattr(self, "_device_tables", None) and self._copy_stream is not None:
+            # the dropped tables' memory returns to the compute stream: order it after their copies
+            torch.cuda.current_stream(self._target_device()).wait_stream(self._copy_stream)
+        self._device_tables: dict[tuple[str, int], torch.Tensor] = {}
         self._reset_staged()
 
     def _reset_staged(self) -> None:
@@ -717,6 +755,7 @@ class MoeRoutingReplayController:
         self._targets: dict[tuple[str, str, int], torch.Tensor] = {}
         self._installed: dict[str, tuple[str, int]] = {}
         self._host_staging: list[torch.Tensor] = []
+        self._device_rows: dict[tuple[str, bool], torch.Tensor] = {}
         self._copy_event: torch.cuda.Event | None = None
         self._copy_waited = True
         self._active_uid_key: str | None = None
@@ -1012,6 +1051,7 @@ class MoeRoutingReplayController:
         if not self._bindings:
             self._active_uid_key = active_token_uid_key
             return
+        use_device = self.device_targets and self._target_device().type == "cuda"
         for uk, uids in sets.items():
             for rk in self._local_router_keys:
                 calls = self._active_calls(rk)
@@ -1021,6 +1061,10 @@ class MoeRoutingReplayController:
                 b = self._bindings[rk]
                 router_uids = self._token_uids_for_router_binding(
                     uids, sequence_parallel=b.sequence_parallel)
+                if use_device and bool((router_uids >= 0).all()):
+                    # padded uids (< 0) take synthetic rows: those micros stay on the host path
+                    self._stage_device((uk, rk, calls[0]), router_uids, b.sequence_parallel)
+                    continue
                 target = self._explicit_target_for_router_call(
                     router_key=rk, call_index=calls[0], explicit_uids=router_uids)
                 self._stage((uk, rk, calls[0]), target)
@@ -1133,6 +1177,38 @@ class MoeRoutingReplayController:
             buf.copy_(host, non_blocking=True)
         self._targets[key] = buf
         self._copy_waited = False
+
+    def _copy_to_device(self, host: torch.Tensor) -> torch.Tensor:
+        """Start an async copy of ``host`` (pinned) into a new device buffer on
+        the side stream; the buffer belongs to the compute stream."""
+        dev = self._target_device()
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(device=dev)
+        host = host.contiguous()
+        host = host if host.is_pinned() else host.pin_memory()
+        self._host_staging.append(host)
+        buf = torch.empty(host.shape, dtype=host.dtype, device=dev)
+        self._copy_stream.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(self._copy_stream):
+            buf.copy_(host, non_blocking=True)
+        self._copy_waited = False
+        return buf
+
+    def _stage_device(self, key: tuple[str, str, int], uids: torch.Tensor,
+                      sequence_parallel: bool) -> None:
+        """Device path: the step's route table of the call (uploaded once per
+        step) and the micro's row map (uploaded once per token layout)."""
+        uk, rk, ci = key
+        table = self._device_tables.get((rk, ci))
+        if table is None:
+            route = self._step_routes.routers[rk].calls[ci]
+            table = self._copy_to_device(route.expert_indices.to(torch.int32))
+            self._device_tables[(rk, ci)] = table
+        rows = self._device_rows.get((uk, sequence_parallel))
+        if rows is None:
+            rows = self._copy_to_device(self._rows_for_uids(uids, rk, ci).to(torch.int32))
+            self._device_rows[(uk, sequence_parallel)] = rows
+        self._targets[key] = DeviceReplayTarget(table, rows)
 
     def wait_for_staged_targets(self) -> None:
         if self._copy_event is None or self._copy_waited:

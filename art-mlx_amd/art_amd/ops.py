@@ -45,8 +45,12 @@ def router_topk(logits: torch.Tensor, k: int):
     return idx, w
 
 
-def router_replay(logits: torch.Tensor, target: torch.Tensor, status: torch.Tensor | None = None):
-    """Replay ``target`` [T,k] ids.  Returns (idx, w, status); status counts rejected ids."""
+def router_replay(logits: torch.Tensor, target, status: torch.Tensor | None = None):
+    """Replay ``target`` [T,k] ids.  Returns (idx, w, status); status counts rejected ids.
+    A target carrying ``table`` and ``rows`` (a device route table and row map,
+    e.g. ``routing_replay.DeviceReplayTarget``) replays ``table[rows[t]]``."""
+    if hasattr(target, "table") and hasattr(target, "rows"):
+        return router_replay_rows(logits, target.table, target.rows, status)
     _cuda(logits, target)
     _need(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be fp32 [T, E]")
     _need(target.dim() == 2 and target.shape[0] == logits.shape[0], "target must be [T, k]")
@@ -60,6 +64,28 @@ def router_replay(logits: torch.Tensor, target: torch.Tensor, status: torch.Tens
         status = torch.zeros(1, dtype=torch.int32, device=logits.device)
     call("art_moe_router_replay", ptr(logits), ptr(target), t, e, k, ptr(idx), ptr(w), ptr(status),
          stream_ptr(logits.device))
+    return idx, w, status
+
+
+def router_replay_rows(logits: torch.Tensor, table: torch.Tensor, rows: torch.Tensor,
+                       status: torch.Tensor | None = None):
+    """Replay ``table[rows[t]]`` (table int32 [N, k] and rows int32 [T] on the
+    device; a row outside [0, N) rejects the token's ids).  Returns (idx, w, status)."""
+    _cuda(logits, table, rows)
+    _need(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be fp32 [T, E]")
+    _need(table.dtype == torch.int32 and table.dim() == 2 and table.is_contiguous(),
+          "table must be contiguous int32 [N, k]")
+    _need(rows.dtype == torch.int32 and rows.dim() == 1 and rows.is_contiguous()
+          and rows.shape[0] == logits.shape[0], "rows must be contiguous int32 [T]")
+    logits = logits.contiguous()
+    t, e = logits.shape
+    k = table.shape[1]
+    idx = torch.empty((t, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    if status is None:
+        status = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    call("art_moe_router_replay_rows", ptr(logits), ptr(table), table.shape[0], ptr(rows), t, e, k,
+         ptr(idx), ptr(w), ptr(status), stream_ptr(logits.device))
     return idx, w, status
 
 

@@ -100,15 +100,27 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(
 }
 
 // Replay: lane j < k of the token's wave takes target[t, j].
+// The target row of token t is target[t, :] (int64), or, with a row map,
+// table[rows[t], :] (int32 [n_rows, k]; a row outside the table rejects all
+// k ids of the token).
 __global__ __launch_bounds__(256) void replay_kernel(
     const float *__restrict__ logits, const int64_t *__restrict__ target,
+    const int32_t *__restrict__ table, int64_t n_rows, const int32_t *__restrict__ rows,
     int64_t T, int E, int k, int32_t *__restrict__ idx, float *__restrict__ w,
     int32_t *__restrict__ status) {
   const int lane = lane_id();
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const bool act = lane < k;
-  int64_t e = act ? target[t * k + lane] : -1;
+  int64_t e = -1;
+  if (act) {
+    if (rows) {
+      const int64_t r = rows[t];
+      e = (r >= 0 && r < n_rows) ? (int64_t)table[r * k + lane] : -1;
+    } else {
+      e = target[t * k + lane];
+    }
+  }
   bool valid = act && e >= 0 && e < E;
   // Repeated id in a row: every later occurrence is rejected.
   for (int j = 0; j < k; ++j) {
@@ -700,9 +712,25 @@ extern "C" int art_moe_router_replay(const float *logits, const int64_t *target,
   ART_REQUIRE(k >= 1 && k <= E && k <= kMaxK, "router_replay: need 1 <= k <= min(E, 32) (k=%d)", k);
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(logits && target && idx && w && status, "router_replay: null pointer");
-  replay_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(logits, target, T, E, k,
-                                                                             idx, w, status);
+  replay_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      logits, target, nullptr, 0, nullptr, T, E, k, idx, w, status);
   return check_launch("router_replay");
+}
+
+extern "C" int art_moe_router_replay_rows(const float *logits, const int32_t *table,
+                                          int64_t n_rows, const int32_t *rows, int64_t T,
+                                          int32_t E, int32_t k, int32_t *idx, float *w,
+                                          int32_t *status, void *stream) {
+  clear_error();
+  ART_REQUIRE(T >= 0 && n_rows >= 0 && E >= 1, "router_replay_rows: need T, n_rows >= 0 and E >= 1");
+  ART_REQUIRE(k >= 1 && k <= E && k <= kMaxK, "router_replay_rows: need 1 <= k <= min(E, 32) (k=%d)",
+              k);
+  if (T == 0) return ART_MOE_OK;
+  ART_REQUIRE(logits && rows && idx && w && status && (table || n_rows == 0),
+              "router_replay_rows: null pointer");
+  replay_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
+      logits, nullptr, table, n_rows, rows, T, E, k, idx, w, status);
+  return check_launch("router_replay_rows");
 }
 
 extern "C" int art_moe_router_backward(const float *dp_part, int32_t n_part, int64_t M,

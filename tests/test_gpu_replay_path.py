@@ -41,7 +41,11 @@ def _bundle(rows, num_experts, tmp_path):
     return RR.MoeRoutingReplayBundle.from_dir(tmp_path)
 
 
-def test_controller_targets_drive_hip_router_and_layer(device, tmp_path):
+@pytest.mark.parametrize("device_targets", [False, True])
+def test_controller_targets_drive_hip_router_and_layer(device, tmp_path, device_targets):
+    """Host path (host-gathered [T, k] target per router call) and device path
+    (route table once per step + row map once per micro, replayed by the
+    row-map kernel) give the same routing."""
     from art_amd import ops
     from art_amd.megatron import routing_replay as RR
     from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
@@ -52,7 +56,8 @@ def test_controller_targets_drive_hip_router_and_layer(device, tmp_path):
     rows = zipf_targets(t, e, k, seed=3)          # Zipf(1.2) ids, some experts empty
     bundle = _bundle(rows, e, tmp_path)
     router = TopKRouter(h, e, k, moe_enable_routing_replay=True, device=device)
-    ctl = RR.MoeRoutingReplayController(bundle=bundle, strict=True, device=device)
+    ctl = RR.MoeRoutingReplayController(bundle=bundle, strict=True, device=device,
+                                        device_targets=device_targets)
     ctl.install_router_patches([_Chunk(router)])
     ctl.set_step(step_index=0, sample_index=[0])
     ctl.begin_micro(0, 0)
@@ -63,7 +68,12 @@ def test_controller_targets_drive_hip_router_and_layer(device, tmp_path):
     logits = router.gating(x)
     probs, rmap = router.routing(logits)
     want = rows[uids]
-    assert torch.equal(router.router_replay.target_topk_idx.cpu(), want)
+    staged = router.router_replay.target_topk_idx
+    assert isinstance(staged, RR.DeviceReplayTarget) == device_targets
+    if device_targets:
+        assert staged.shape == (1500, k) and staged.table.shape == (t, k)
+        staged = staged.materialize()
+    assert torch.equal(staged.cpu(), want)
     exp_map = torch.zeros((1500, e), dtype=torch.bool)
     exp_map[torch.arange(1500).unsqueeze(1), want] = True
     assert torch.equal(rmap.cpu(), exp_map)

@@ -236,3 +236,25 @@ def test_router_lora_grad_matches_fp32(device, t, k, r, e):
         dlog_ref[sel, idx[sel, j].long()] += dl[sel, j].double()
     torch.testing.assert_close(g.cpu().double(), g_ref, rtol=2 ** -7, atol=1e-4)
     torch.testing.assert_close(dlog.cpu().double(), dlog_ref, rtol=2 ** -7, atol=1e-4)
+
+
+def test_router_replay_rows_equals_gathered_target(device):
+    """Replay of table[rows[t]] is bit-exact with replaying the gathered
+    target; rows outside the table reject the token's k ids (status counts
+    them) like out-of-range ids do."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(21)
+    n, t, e, k = 5000, 3000, 96, 6
+    table = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)]).to(torch.int32)
+    table[7, 1] = table[7, 0]                       # a repeated id inside one row
+    rows = torch.randint(0, n, (t,), generator=g, dtype=torch.int32)
+    rows[[3, 10, 2999]] = torch.tensor([-1, n, 7], dtype=torch.int32)
+    logits = torch.randn(t, e, generator=g)
+    idx_r, w_r, st_r = ops.router_replay_rows(logits.to(device), table.to(device), rows.to(device))
+    tgt = table[rows.clamp(0, n - 1).long()].long()
+    tgt[3] = -1
+    tgt[10] = -1
+    idx_t, w_t, st_t = ops.router_replay(logits.to(device), tgt.to(device))
+    assert torch.equal(idx_r.cpu(), idx_t.cpu()) and torch.equal(w_r.cpu(), w_t.cpu())
+    assert int(st_r.item()) == int(st_t.item()) == 2 * k + 1
+    assert (idx_r[3] == -1).all() and (idx_r[10] == -1).all() and int(idx_r[2999, 1]) == -1

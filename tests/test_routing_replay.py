@@ -410,3 +410,21 @@ def test_controller_legacy_call_order_without_micro_metadata():
     with pytest.raises(RuntimeError, match="lacks sample metadata"):
         c.set_step(step_index=0, sample_index=None)
     c.remove_router_patches()
+
+
+def test_device_replay_target_wrapper_and_cpu_fallback():
+    """DeviceReplayTarget reads table[rows]; on a CPU device the controller's
+    device path falls back to host targets (the device path needs a GPU)."""
+    table = torch.tensor([[1, 2], [3, 0], [2, 1]], dtype=torch.int32)
+    rows = torch.tensor([2, 0, 0, 1], dtype=torch.int32)
+    d = RR.DeviceReplayTarget(table, rows)
+    assert d.shape == (4, 2)
+    assert torch.equal(d.materialize(), torch.tensor([[2, 1], [1, 2], [1, 2], [3, 0]]))
+    scores = torch.arange(16, dtype=torch.float32).reshape(4, 4)
+    rr = RR.RouterReplay()
+    rr.set_target_indices(d)
+    rr.set_router_replay_action(RR.RouterReplayAction.REPLAY_FORWARD)
+    vals, ids = rr.get_replay_topk(scores, 2)
+    assert torch.equal(ids, d.materialize()) and torch.equal(vals, scores.gather(1, ids))
+    with pytest.raises(RuntimeError, match="table"):
+        RR.DeviceReplayTarget(table, rows.view(2, 2))
