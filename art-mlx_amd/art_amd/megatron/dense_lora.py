@@ -1,0 +1,281 @@
+"""Dense (non-expert) LoRA linears on the HIP grouped products.
+
+The shared-expert FC1 / FC2, attention output projection and QKV LoRA of
+/root/reference/src/art/megatron/lora.py:1167-1395, 1574-1650 run as a
+one-segment instance of the expert layer's fused design:
+
+    y = x W^T + sum_i s_i (x A_i) B_i        (B_i's outputs placed at columns C_i)
+
+* forward: t = x [A_1 | A_2 | ...] (one narrow product, each rank padded to
+  the 16-wide MFMA step), then y = x W^T + t L^T in ONE launch: the LoRA
+  terms are extra K-steps of the base product's accumulators, with
+  L [out, R] holding s_i B_i^T at the rows C_i;
+* backward: g = dy L (narrow), dx = dy W + g [A_1 | ...]^T (one launch, the
+  same K-extension), dA_i = x^T g_i and dB_i = s_i t_i^T dy[:, C_i] from the
+  segmented TN kernel (dB as (dy^T t)^T, so that the wide output dimension
+  takes the kernel's P tiles and the rank its Q tiles).
+
+Output placements cover the reference's layouts: a contiguous column range
+(projection, the gate and up halves of FC1) and the grouped-query QKV packing,
+where every query group holds [q heads (times 2 with an output gate) | k | v]
+(lora.py:1344-1395).  Base weights are frozen bf16 [out, in]; tensor-parallel
+reductions are out of scope (one GPU).  Where the reference's base linear fuses
+the input layernorm and hands its output to the adapters (lora.py:1368-1375),
+these modules take that normalised activation as ``x``: base and LoRA both
+read it, as in the reference.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .. import ops
+from .kernels.grouped_lora_hip import padded_rank
+from .lora import LoRA
+
+
+@dataclass(frozen=True)
+class Placement:
+    """Output columns {g * period + offset + j : g < groups, j < width}."""
+    groups: int
+    period: int
+    offset: int
+    width: int
+
+    @staticmethod
+    def columns(start: int, width: int, total: int) -> "Placement":
+        """Columns start .. start + width of a ``total``-wide output."""
+        return Placement(1, total, start, width)
+
+    @property
+    def out_features(self) -> int:
+        return self.groups * self.width
+
+
+_SEGS: dict = {}
+
+
+def _segments(t: int, pieces: int, device) -> torch.Tensor:
+    """Segment table of ``t`` rows cut into ``pieces`` near-equal segments
+    (cached: a handful of (t, pieces) pairs recur every step)."""
+    key = (t, pieces, str(device))
+    seg = _SEGS.get(key)
+    if seg is None:
+        if len(_SEGS) > 64:
+            _SEGS.clear()
+        base, extra = divmod(t, pieces)
+        seg = _SEGS[key] = ops.segments_from_counts(
+            [base + (i < extra) for i in range(pieces)], pieces, device)
+    return seg
+
+
+def _wgrad_rows(lm: torch.Tensor, r: torch.Tensor) -> torch.Tensor:
+    """fp32 ``lm^T r`` summed over every row.
+
+    The segmented TN kernel gives each segment's 2048-row chunks one workgroup
+    per output tile, which leaves most of the chip idle for one long segment
+    and a narrow output.  The rows are therefore cut into equal pieces (each one
+    chunk, written straight to its own slice) so that pieces x tiles fills the
+    CUs, and the pieces are summed in a fixed order: deterministic, no atomics.
+    Tile sizes follow the kernel's choice (wgrad.hip: wgrad_bq, wg_bp)."""
+    t, p = lm.shape
+    q = r.shape[1]
+    bq = 16 if q <= 16 else 32 if q <= 32 else 64 if q <= 64 else 128
+    bp = 256 if bq >= 64 else 128
+    tiles = -(-p // bp) * -(-q // bq)
+    pieces = max(1, min(-(-t // 256), max(-(-t // 2048), -(-512 // tiles))))
+    out = ops.grouped_wgrad(lm, r, _segments(t, pieces, lm.device), pieces)
+    return out[0] if pieces == 1 else out.sum(0)
+
+
+class _DenseLoRAFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x2, lin: "DenseLoRALinear", *factors):
+        segs = lin.segments
+        t, d_in = x2.shape
+        d_out = lin.out_features
+        rps = [padded_rank(int(f.shape[-1])) for f in factors[0::2]]
+        c0s = [sum(rps[:i]) for i in range(len(rps))]
+        rp = sum(rps)
+        dev = x2.device
+        seg1 = _segments(t, 1, dev)
+        a_cat = x2.new_empty((1, rp, d_in))
+        l_mat = x2.new_zeros((1, d_out, rp))
+        items = []
+        for (lora, pl), a_t, b_t, c0, rpi in zip(segs, factors[0::2], factors[1::2], c0s, rps):
+            r = int(a_t.shape[-1])
+            items.append((a_cat[:, c0:c0 + rpi, :], a_t.t().unsqueeze(0), 1.0))
+            dst = l_mat[0].view(pl.groups, pl.period, rp)[:, pl.offset:pl.offset + pl.width,
+                                                          c0:c0 + rpi]
+            items.append((dst, b_t.view(r, pl.groups, pl.width).permute(1, 2, 0), float(lora.scale)))
+        for i in range(0, len(items), 16):
+            ops.pack(*items[i:i + 16])
+        tl = ops.grouped_gemm(x2, a_cat, seg1, 1, m=t)
+        y = ops.grouped_gemm(x2, lin.weight.unsqueeze(0), seg1, 1, m=t, tl=tl, l=l_mat)
+        ctx.save_for_backward(x2, tl, *factors)
+        ctx.lin, ctx.rps, ctx.c0s, ctx.seg1 = lin, rps, c0s, seg1
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, tl, *factors = ctx.saved_tensors
+        lin, rps, c0s, seg1 = ctx.lin, ctx.rps, ctx.c0s, ctx.seg1
+        dy = dy.contiguous()
+        t, d_in = x2.shape
+        rp = sum(rps)
+        lt = dy.new_zeros((1, rp, lin.out_features))
+        a_cat_t = dy.new_empty((1, d_in, rp))
+        items = []
+        for (lora, pl), a_t, b_t, c0, rpi in zip(lin.segments, factors[0::2], factors[1::2], c0s, rps):
+            r = int(a_t.shape[-1])
+            # rows c0 + r .. c0 + rpi stay zero (lt is zero-filled)
+            dst = lt[0].view(rp, pl.groups, pl.period)[c0:c0 + r, :, pl.offset:pl.offset + pl.width]
+            items.append((dst, b_t.view(r, pl.groups, pl.width), float(lora.scale)))
+            items.append((a_cat_t[:, :, c0:c0 + rpi], a_t.unsqueeze(0), 1.0))
+        for i in range(0, len(items), 16):
+            ops.pack(*items[i:i + 16])
+        g = ops.grouped_gemm(dy, lt, seg1, 1, m=t)                          # [T, rp]
+        dx = ops.grouped_gemm(dy, lin.weight_t.unsqueeze(0), seg1, 1, m=t, tl=g, l=a_cat_t)
+        g_a = _wgrad_rows(x2, g)                                            # [in, rp] fp32
+        g_b = _wgrad_rows(dy, tl).t()                                       # [rp, out] fp32 view
+        grads = []
+        for (lora, pl), a_t, b_t, c0 in zip(lin.segments, factors[0::2], factors[1::2], c0s):
+            r = int(a_t.shape[-1])
+            grads.append(g_a[:, c0:c0 + r].to(a_t.dtype))
+            gb = g_b.unflatten(1, (pl.groups, pl.period))[c0:c0 + r, :, pl.offset:pl.offset + pl.width]
+            grads.append((float(lora.scale) * gb.reshape(r, pl.out_features)).to(b_t.dtype))
+        return (dx, None, *grads)
+
+
+class DenseLoRALinear(torch.nn.Module):
+    """Frozen bf16 linear ``weight [out, in]`` with LoRA adapters placed at
+    output columns: ``segments`` lists ``(LoRA, Placement)`` (one expert each,
+    ``A_T [in, r]``, ``B_T [r, out_i]``)."""
+
+    def __init__(self, weight: torch.Tensor, segments: list[tuple[LoRA, Placement]]) -> None:
+        super().__init__()
+        self.out_features, self.in_features = (int(d) for d in weight.shape)
+        self.register_buffer("weight", weight.detach().contiguous())
+        self._weight_t: torch.Tensor | None = None
+        self.segments = segments
+        for i, (lora, pl) in enumerate(segments):
+            if lora.A_T.dim() != 2:
+                raise ValueError("dense LoRA segments hold one expert (A_T [in, r])")
+            if lora.A_T.shape[0] != self.in_features or lora.B_T.shape[1] != pl.out_features:
+                raise ValueError(f"segment {i}: LoRA shapes {tuple(lora.A_T.shape)}, "
+                                 f"{tuple(lora.B_T.shape)} do not fit in={self.in_features}, "
+                                 f"out={pl.out_features}")
+            if pl.groups * pl.period != self.out_features or pl.offset + pl.width > pl.period:
+                raise ValueError(f"segment {i}: placement {pl} does not tile {self.out_features} "
+                                 "output columns")
+            self.add_module(f"lora{i}", lora)
+
+    @property
+    def weight_t(self) -> torch.Tensor:
+        if self._weight_t is None or self._weight_t.device != self.weight.device:
+            self._weight_t = ops.transposed(self.weight.unsqueeze(0))[0]
+        return self._weight_t
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        lead = x.shape[:-1]
+        factors = [p for lora, _ in self.segments for p in (lora.A_T, lora.B_T)]
+        if x.numel() == 0:
+            zero = x.sum() * 0.0
+            for p in factors:
+                zero = zero + p.to(x.dtype).sum() * 0.0
+            return zero.expand(*lead, self.out_features).clone()
+        y = _DenseLoRAFn.apply(x.reshape(-1, self.in_features).contiguous(), self, *factors)
+        return y.view(*lead, self.out_features)
+
+
+def _lora(prefix: str, d_in: int, d_out: int, rank: int, alpha: float, weight: torch.Tensor) -> LoRA:
+    return LoRA(prefix, d_in, d_out, rank, alpha, weight.dtype, weight.device)
+
+
+class SelfAttentionLinearProjLoRA(torch.nn.Module):
+    """Attention output projection + LoRA (lora.py:1167-1201):
+    ``forward(x) -> (base + lora, None)``."""
+
+    def __init__(self, adapter_model_prefix: str, weight: torch.Tensor, rank: int,
+                 alpha: float) -> None:
+        super().__init__()
+        d_out, d_in = (int(d) for d in weight.shape)
+        self.lora = _lora(adapter_model_prefix, d_in, d_out, rank, alpha, weight)
+        self.linear = DenseLoRALinear(weight, [(self.lora, Placement.columns(0, d_out, d_out))])
+
+    def forward(self, x: torch.Tensor):
+        return self.linear(x), None
+
+
+class SharedExpertsLinearFC1LoRA(torch.nn.Module):
+    """Shared-expert FC1 (gate | up halves) + gate and up LoRA
+    (lora.py:1574-1626): ``forward(x) -> (base + [gate | up], None)``."""
+
+    def __init__(self, adapter_model_prefix: str, weight: torch.Tensor, rank: int,
+                 alpha: float) -> None:
+        super().__init__()
+        d_out, d_in = (int(d) for d in weight.shape)
+        if d_out % 2:
+            raise ValueError("shared-expert FC1 needs an even output width (gate | up)")
+        f = d_out // 2
+        self.gate_lora = _lora(f"{adapter_model_prefix}.gate_proj", d_in, f, rank, alpha, weight)
+        self.up_lora = _lora(f"{adapter_model_prefix}.up_proj", d_in, f, rank, alpha, weight)
+        self.linear = DenseLoRALinear(weight, [(self.gate_lora, Placement.columns(0, f, d_out)),
+                                               (self.up_lora, Placement.columns(f, f, d_out))])
+
+    def forward(self, x: torch.Tensor):
+        return self.linear(x), None
+
+
+class SharedExpertsLinearFC2LoRA(torch.nn.Module):
+    """Shared-expert FC2 + down LoRA (lora.py:1629-1649)."""
+
+    def __init__(self, adapter_model_prefix: str, weight: torch.Tensor, rank: int,
+                 alpha: float) -> None:
+        super().__init__()
+        self.row_parallel_lora = SelfAttentionLinearProjLoRA(f"{adapter_model_prefix}.down_proj",
+                                                             weight, rank, alpha)
+
+    def forward(self, x: torch.Tensor):
+        return self.row_parallel_lora(x)
+
+
+class SelfAttentionLinearQKVLoRA(torch.nn.Module):
+    """Packed QKV projection + q/k/v LoRA (lora.py:1204-1395): the output
+    holds, per query group, [q heads (x2 with ``attention_output_gate``) | k |
+    v] of ``kv_channels`` each; the q, k and v adapters land in their slots of
+    every group.  Modules missing from ``target_modules`` get no adapter."""
+
+    def __init__(self, adapter_model_prefix: str, weight: torch.Tensor, rank: int, alpha: float,
+                 *, num_attention_heads: int, num_query_groups: int, kv_channels: int,
+                 attention_output_gate: bool = False,
+                 target_modules: set[str] | None = None) -> None:
+        super().__init__()
+        if num_attention_heads % num_query_groups:
+            raise ValueError("num_attention_heads must be divisible by num_query_groups for QKV LoRA")
+        targets = {"q_proj", "k_proj", "v_proj"} if target_modules is None else set(target_modules)
+        d_out, d_in = (int(d) for d in weight.shape)
+        hpg = num_attention_heads // num_query_groups
+        qw = hpg * kv_channels * (2 if attention_output_gate else 1)
+        period = qw + 2 * kv_channels
+        if d_out != num_query_groups * period:
+            raise ValueError(f"QKV weight has {d_out} rows, the packing needs "
+                             f"{num_query_groups * period}")
+        self.num_query_groups_per_partition = num_query_groups
+        self.q_and_gate_out_features_per_rank = num_query_groups * qw
+        self.kv_out_features_per_rank = num_query_groups * kv_channels
+        segs = []
+        self.q_proj_lora = self.k_proj_lora = self.v_proj_lora = None
+        for name, off, width in (("q_proj", 0, qw), ("k_proj", qw, kv_channels),
+                                 ("v_proj", qw + kv_channels, kv_channels)):
+            if name not in targets:
+                continue
+            lora = _lora(f"{adapter_model_prefix}.{name}", d_in, num_query_groups * width, rank,
+                         alpha, weight)
+            setattr(self, f"{name}_lora", lora)
+            segs.append((lora, Placement(num_query_groups, period, off, width)))
+        self.linear = DenseLoRALinear(weight, segs)
+
+    def forward(self, x: torch.Tensor):
+        return self.linear(x), None

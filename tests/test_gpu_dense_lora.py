@@ -1,0 +1,107 @@
+"""Dense LoRA linears (shared-expert FC1/FC2, attention projection, QKV) on the
+HIP products against a plain fp32 torch reference on the CPU.
+
+Bar: outputs and gradients (dx, dA, dB) within 2e-2 relative (bf16 operands,
+fp32 accumulation); empty input keeps the graph and returns zeros.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _randomise(loras, g):
+    with torch.no_grad():
+        for lora in loras:
+            lora.B_T.copy_((torch.randn(lora.B_T.shape, generator=g) * 0.05).to(lora.B_T.dtype))
+
+
+def _check(module, loras, placements, x, g):
+    """Run module fwd/bwd on the GPU and the fp32 reference y = x W^T +
+    sum s (x A) B placed at the given output columns."""
+    weight = module.linear.weight
+    dy = torch.randn((*x.shape[:-1], weight.shape[0]), generator=g).to(torch.bfloat16)
+    xd = x.to(weight.device).requires_grad_()
+    y, bias = module(xd)
+    assert bias is None
+    y.backward(dy.to(weight.device))
+    xr = x.float().requires_grad_()
+    leaves = [(l.A_T.detach().cpu().float().requires_grad_(),
+               l.B_T.detach().cpu().float().requires_grad_()) for l in loras]
+    yr = xr @ weight.cpu().float().T
+    for (a, b), l, cols in zip(leaves, loras, placements):
+        add = torch.zeros_like(yr)
+        add[..., cols] = l.scale * (xr @ a) @ b
+        yr = yr + add
+    yr.backward(dy.float())
+    assert rel(y.detach(), yr.detach()) < 2e-2
+    assert rel(xd.grad, xr.grad) < 2e-2
+    for (a, b), l in zip(leaves, loras):
+        assert rel(l.A_T.grad, a.grad) < 2e-2 and rel(l.B_T.grad, b.grad) < 2e-2
+
+
+def test_projection_and_shared_expert_fc2(device):
+    from art_amd.megatron.dense_lora import SelfAttentionLinearProjLoRA, SharedExpertsLinearFC2LoRA
+    g = torch.Generator().manual_seed(1)
+    w = (torch.randn(384, 512, generator=g) * 0.03).to(torch.bfloat16).to(device)
+    proj = SelfAttentionLinearProjLoRA("layers.0.self_attn.o_proj", w, 16, 32)
+    _randomise([proj.lora], g)
+    x = torch.randn(3, 700, 512, generator=g).to(torch.bfloat16)      # [seq, batch, hidden]
+    _check(proj, [proj.lora], [slice(0, 384)], x, g)
+    fc2 = SharedExpertsLinearFC2LoRA("layers.0.mlp.shared_expert", w, 8, 16)
+    assert fc2.row_parallel_lora.lora.adapter_model_prefix.endswith("shared_expert.down_proj")
+    _randomise([fc2.row_parallel_lora.lora], g)
+    _check(fc2.row_parallel_lora, [fc2.row_parallel_lora.lora], [slice(0, 384)],
+           torch.randn(2100, 512, generator=g).to(torch.bfloat16), g)
+
+
+def test_shared_expert_fc1_gate_up(device):
+    from art_amd.megatron.dense_lora import SharedExpertsLinearFC1LoRA
+    g = torch.Generator().manual_seed(2)
+    f, h = 320, 256
+    w = (torch.randn(2 * f, h, generator=g) * 0.03).to(torch.bfloat16).to(device)
+    fc1 = SharedExpertsLinearFC1LoRA("layers.1.mlp.shared_expert", w, 24, 48)
+    _randomise([fc1.gate_lora, fc1.up_lora], g)
+    _check(fc1, [fc1.gate_lora, fc1.up_lora], [slice(0, f), slice(f, 2 * f)],
+           torch.randn(1000, h, generator=g).to(torch.bfloat16), g)
+
+
+@pytest.mark.parametrize("gate,targets", [(False, None), (True, None), (False, {"q_proj", "v_proj"})])
+def test_qkv_grouped_query_packing(device, gate, targets):
+    from art_amd.megatron.dense_lora import SelfAttentionLinearQKVLoRA
+    g = torch.Generator().manual_seed(3)
+    heads, groups, d, h = 8, 2, 64, 512
+    hpg = heads // groups
+    qw = hpg * d * (2 if gate else 1)
+    period = qw + 2 * d
+    w = (torch.randn(groups * period, h, generator=g) * 0.03).to(torch.bfloat16).to(device)
+    qkv = SelfAttentionLinearQKVLoRA("layers.2.self_attn", w, 16, 32, num_attention_heads=heads,
+                                     num_query_groups=groups, kv_channels=d,
+                                     attention_output_gate=gate, target_modules=targets)
+    loras, cols = [], []
+    for name, off, width in (("q_proj", 0, qw), ("k_proj", qw, d), ("v_proj", qw + d, d)):
+        lora = getattr(qkv, f"{name}_lora")
+        if targets is not None and name not in targets:
+            assert lora is None
+            continue
+        loras.append(lora)
+        cols.append(torch.cat([torch.arange(gi * period + off, gi * period + off + width)
+                               for gi in range(groups)]))
+    _randomise(loras, g)
+    _check(qkv, loras, cols, torch.randn(777, h, generator=g).to(torch.bfloat16), g)
+
+
+def test_empty_input_keeps_graph(device):
+    from art_amd.megatron.dense_lora import SharedExpertsLinearFC1LoRA
+    w = torch.zeros(128, 64, dtype=torch.bfloat16, device=device)
+    fc1 = SharedExpertsLinearFC1LoRA("p", w, 8, 16)
+    x = torch.zeros(0, 64, dtype=torch.bfloat16, device=device, requires_grad=True)
+    y, _ = fc1(x)
+    assert y.shape == (0, 128) and y.requires_grad
+    y.sum().backward()
+    assert fc1.gate_lora.A_T.grad is not None
