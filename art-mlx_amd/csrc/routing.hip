@@ -304,22 +304,26 @@ constexpr int kMaxK = 32;
 __global__ __launch_bounds__(256) void combine_kernel(
     const U4 *__restrict__ yp, const int32_t *__restrict__ dest, const float *__restrict__ wgt,
     const float *__restrict__ dl, const int32_t *__restrict__ idx, const U4 *__restrict__ w_r,
-    const U4 *__restrict__ addend, int64_t T, int k, int H8, U4 *__restrict__ y) {
+    const U4 *__restrict__ addend, int64_t T, int k, int H8, int n_chunks, U4 *__restrict__ y) {
   const int lane = lane_id();
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // One wavefront per (token, 64-lane chunk of the row): short waves that
+  // keep many rows in flight and leave no long tail when the grid is a
+  // fraction of a round over the resident waves.
+  const int64_t wv = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t t = wv / n_chunks;
   if (t >= T) return;
+  const int c0 = (int)(wv - t * n_chunks) * kWave;
   const bool act = lane < k;
   const int my_dest = act ? dest[t * k + lane] : -1;
   const float my_w = (act && wgt) ? wgt[t * k + lane] : 1.0f;
   const int my_e = (act && w_r) ? idx[t * k + lane] : -1;
   const float my_dl = (act && w_r) ? dl[t * k + lane] : 0.0f;
-  // The chunk loop is uniform across the wavefront (every lane runs every
-  // iteration) so that the slot broadcasts below always read active lanes.
-  // Slots go in blocks of 8 whose row loads are all issued before the first
-  // is accumulated (8 loads in flight per lane instead of a chain of k); the
-  // accumulation order stays slot-ascending.  Slot j >= k reads lane j's
-  // inactive dest (-1).
-  for (int c0 = 0; c0 < H8; c0 += kWave) {
+  // Every lane of the wavefront runs the slot loops (uniform), so the slot
+  // broadcasts below always read active lanes.  Slots go in blocks of 8
+  // whose row loads are all issued before the first is accumulated (8 loads
+  // in flight per lane instead of a chain of k); the accumulation order
+  // stays slot-ascending.  Slot j >= k reads lane j's inactive dest (-1).
+  {
     const int c = c0 + lane;
     const bool on = c < H8;
     float acc[8];
@@ -828,9 +832,12 @@ extern "C" int art_moe_combine(const void *y_perm, const int32_t *dest, const fl
               "combine: need H %% 8 == 0 and 1 <= k <= 32 (H=%d k=%d)", H, k);
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(y_perm && dest && y && (!w_r || (dl && idx)), "combine: null pointer");
-  combine_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
+  const int n_chunks = (H / 8 + kWave - 1) / kWave;
+  const int64_t blocks = (T * n_chunks + 3) / 4;
+  ART_REQUIRE(blocks < ((int64_t)1 << 31), "combine: T * H too large (T=%lld H=%d)", (long long)T, H);
+  combine_kernel<<<dim3((unsigned)blocks), 256, 0, as_stream(stream)>>>(
       (const U4 *)y_perm, dest, wgt, dl, idx, (const U4 *)w_r, (const U4 *)addend, T, k, H / 8,
-      (U4 *)y);
+      n_chunks, (U4 *)y);
   return check_launch("combine");
 }
 
