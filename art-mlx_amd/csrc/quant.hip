@@ -7,8 +7,10 @@
 // x W^T with W = q * s per k equals (x * s) q^T.  Each row is scaled by
 // s_row = amax / 448 (1 for an all-zero row), q = e4m3fn(v / s_row) rounded to
 // nearest even, and s_row is stored beside it; q * s_row reproduces v to fp8
-// precision.  Bandwidth-bound: one wavefront per row, two passes over the row
-// (the second from L1/L2), 16-byte loads, 8-byte stores.
+// precision.  Bandwidth-bound: one wavefront per row, 16-byte loads, 8-byte
+// stores; rows of up to 4096 values are held in registers between the row
+// maximum and the quantisation (quant_rows_reg_kernel), longer rows take two
+// passes, the second from L1/L2 (quant_rows_kernel).
 #include "common.h"
 
 namespace art {
@@ -74,6 +76,70 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(
   if (lane == 0) row_scale[m] = s;
 }
 
+// Rows of up to NCH * 512 values: every 16-byte chunk of the lane's share is
+// loaded at once before the row maximum is taken, the column scales are
+// applied once, and the quantisation reads the scaled values from registers:
+// the row and its scales stream from memory once, NCH loads in flight per
+// lane, instead of two dependent passes each reloading data and scales.  Same
+// operations in the same order as quant_rows_kernel, so the codes and scales
+// are identical.
+template <int NCH>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(
+    const bf16 *__restrict__ src, int64_t lds, const int32_t *__restrict__ rows,
+    const int32_t *__restrict__ seg, int E, const float *__restrict__ cs, int64_t cs_es,
+    int64_t M, int K, uint8_t *__restrict__ q, int64_t ldq, float *__restrict__ row_scale) {
+  const int lane = lane_id();
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const bf16 *x = src + (int64_t)(rows ? rows[m] : m) * lds;
+  const float *c = nullptr;
+  if (cs) {  // expert of row m: the last e with seg[e] <= m
+    int lo = 0, hi = E;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (seg[mid] <= m) lo = mid; else hi = mid;
+    }
+    c = cs + (int64_t)lo * cs_es;
+  }
+  U4 v[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int k = (i * kWave + lane) * 8;
+    v[i] = k < K ? *(const U4 *)(x + k) : U4{0u, 0u, 0u, 0u};
+  }
+  float f[NCH][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int k = (i * kWave + lane) * 8;
+    unpack8(v[i], f[i]);  // zeros past K
+    if (c && k < K) {
+      const float4 c0 = *(const float4 *)(c + k), c1 = *(const float4 *)(c + k + 4);
+      f[i][0] *= c0.x; f[i][1] *= c0.y; f[i][2] *= c0.z; f[i][3] *= c0.w;
+      f[i][4] *= c1.x; f[i][5] *= c1.y; f[i][6] *= c1.z; f[i][7] *= c1.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[i][j]));
+  }
+  amax = wave_absmax(amax);
+  const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+  uint8_t *qr = q + m * ldq;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int k = (i * kWave + lane) * 8;
+    if (k >= K) continue;
+    float g[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) g[j] = fminf(fmaxf(f[i][j] / s, -448.0f), 448.0f);
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(g[0], g[1], 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(g[2], g[3], lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(g[4], g[5], 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(g[6], g[7], hi, true);
+    *(uint2 *)(qr + k) = make_uint2((unsigned)lo, (unsigned)hi);
+  }
+  if (lane == 0) row_scale[m] = s;
+}
+
 }  // namespace art
 
 using namespace art;
@@ -96,8 +162,22 @@ extern "C" int art_moe_quantize_rows_fp8(const void *src, int64_t ld_src, const 
     ART_REQUIRE(cs_estride >= K && cs_estride % 4 == 0 && ((uintptr_t)col_scale & 15) == 0,
                 "quantize_rows_fp8: column scales must be 16-byte aligned rows of >= K");
   }
-  quant_rows_kernel<<<dim3((unsigned)((M + 3) / 4)), 256, 0, as_stream(stream)>>>(
-      (const bf16 *)src, ld_src, rows, seg, E, col_scale, cs_estride, M, K, (uint8_t *)q, ldq,
-      row_scale);
+  const dim3 grid((unsigned)((M + 3) / 4));
+  const int nch = (K + kWave * 8 - 1) / (kWave * 8);  // 16-byte chunks per lane
+#define ART_QUANT_REG(N)                                                                      \
+  case N:                                                                                     \
+    quant_rows_reg_kernel<N><<<grid, 256, 0, as_stream(stream)>>>(                            \
+        (const bf16 *)src, ld_src, rows, seg, E, col_scale, cs_estride, M, K, (uint8_t *)q, ldq, \
+        row_scale);                                                                           \
+    break;
+  switch (nch) {
+    ART_QUANT_REG(1) ART_QUANT_REG(2) ART_QUANT_REG(3) ART_QUANT_REG(4)
+    ART_QUANT_REG(5) ART_QUANT_REG(6) ART_QUANT_REG(7) ART_QUANT_REG(8)
+    default:  // rows longer than 4096 values: chunked, two passes
+      quant_rows_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+          (const bf16 *)src, ld_src, rows, seg, E, col_scale, cs_estride, M, K, (uint8_t *)q, ldq,
+          row_scale);
+  }
+#undef ART_QUANT_REG
   return check_launch("quantize_rows_fp8");
 }

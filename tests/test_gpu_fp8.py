@@ -164,11 +164,16 @@ def _ref_quant(v):
     return q, s
 
 
-@pytest.mark.parametrize("gather,cols", [(False, False), (True, False), (True, True)])
-def test_quantize_rows_fp8_matches_torch(device, gather, cols):
+@pytest.mark.parametrize("gather,cols,k", [(False, False, 512), (True, False, 512), (True, True, 512),
+                                           (False, False, 8), (True, True, 1544),
+                                           (False, True, 4096), (True, False, 4104)])
+def test_quantize_rows_fp8_matches_torch(device, gather, cols, k):
+    """Row lengths cover the register-resident kernel (k <= 4096: one 16-byte
+    chunk per lane up to 8, ragged last chunk at 1544) and the two-pass loop
+    kernel beyond (4104)."""
     ops = _ops()
-    g = torch.Generator().manual_seed(7 + gather + 2 * cols)
-    t, k, e = 300, 512, 6
+    g = torch.Generator().manual_seed(7 + gather + 2 * cols + k)
+    t, e = 300, 6
     x = torch.randn(t, k, generator=g).to(torch.bfloat16)
     x[5] = 0  # an all-zero row takes scale 1
     m = 900 if gather else t
