@@ -329,6 +329,15 @@ __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&a
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfv[j], af[i], acc[i][j], 0, 0, 0);
 }
 
+// Row groups of the SwiGLU-backward epilogue: the fewest that divide the
+// wave's TM row blocks and let one group's dg and du (2 x BM/nh rows of BN
+// bf16) fit the LDS ring; 0 when none does.
+constexpr int epi2_groups(int tm, int bm, int bn, int lds_bytes) {
+  for (int nh = 1; nh <= tm; ++nh)
+    if (tm % nh == 0 && 2 * (bm / nh) * bn * 2 <= lds_bytes) return nh;
+  return 0;
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int NW = WM * WN, NT = NW * 64;
@@ -359,6 +368,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 6, "vmcnt range");
   static_assert(LDS_BYTES + RED_BYTES <= 160 * 1024, "LDS of one workgroup");
   static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
+  constexpr int EPI2_NH = EPI == EPI_SWIGLU_BWD ? epi2_groups(TM, BM, BN, LDS_BYTES) : 1;
+  static_assert(EPI2_NH >= 1, "SwiGLU backward staging (dg and du of a row group) must fit the LDS ring");
   static_assert(!W8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
 
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES];
@@ -763,57 +774,74 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         }
       }
     } else {  // EPI_SWIGLU_BWD: acc = dh over columns f of this tile
+      // Rows go in EPI2_NH groups (i = h*TMG .. h*TMG+TMG-1 of every wave):
+      // each group's dg and du are staged side by side (two regions of
+      // BM/EPI2_NH rows) and written out before the next group, so no
+      // register array carries du across the barriers (an all-rows du buffer
+      // pushed the 256-row tiles into spilling inside the k-loop).
+      constexpr int TMG = TM / EPI2_NH, RG = BM / EPI2_NH, WRG = WTM / EPI2_NH;
       const int F = p.F;
-      uint2 du_pk[TM][TN][4];
       float rs[TM];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        rs[i] = 0.0f;
-        const int row = wm * WTM + i * 32 + lrow;
-        const int m = m0 + row;
-        const int mc = m < m_end ? m : m_end - 1;
-        const float pr = p.prob[mc];
-        const bf16 *yr = p.y1_in + (int64_t)mc * (2 * F);
+      for (int h = 0; h < EPI2_NH; ++h) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int ii = 0; ii < TMG; ++ii) {
+          const int i = h * TMG + ii;
+          rs[i] = 0.0f;
+          const int row = wm * WTM + i * 32 + lrow;
+          const int lr = wm * WRG + ii * 32 + lrow;  // row in the group's regions
+          const int m = m0 + row;
+          const int mc = m < m_end ? m : m_end - 1;
+          const float pr = p.prob[mc];
+          const bf16 *yr = p.y1_in + (int64_t)mc * (2 * F);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            int f = nt * BN + wn * WTN + j * 32 + 8 * q + 4 * lk;
-            const bool fin = f < F;
-            f = fin ? f : 0;
-            const uint2 gr = *(const uint2 *)(yr + f);
-            const uint2 ur = *(const uint2 *)(yr + F + f);
-            const float g4[4] = {__uint_as_float(gr.x << 16), __uint_as_float(gr.x & 0xffff0000u),
-                                 __uint_as_float(gr.y << 16), __uint_as_float(gr.y & 0xffff0000u)};
-            const float u4[4] = {__uint_as_float(ur.x << 16), __uint_as_float(ur.x & 0xffff0000u),
-                                 __uint_as_float(ur.y << 16), __uint_as_float(ur.y & 0xffff0000u)};
-            float dg[4], du[4];
+          for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const float dh = p.alpha * acc[i][j][4 * q + v];
-              const float sg = sigmoid_f(g4[v]);
-              const float sl = g4[v] * sg;
-              const float dhp = dh * pr;
-              dg[v] = dhp * u4[v] * sg * (1.0f + g4[v] * (1.0f - sg));
-              du[v] = dhp * sl;
-              if (fin) rs[i] += dh * sl * u4[v];
+            for (int q = 0; q < 4; ++q) {
+              int f = nt * BN + wn * WTN + j * 32 + 8 * q + 4 * lk;
+              const bool fin = f < F;
+              f = fin ? f : 0;
+              const uint2 gr = *(const uint2 *)(yr + f);
+              const uint2 ur = *(const uint2 *)(yr + F + f);
+              const float g4[4] = {__uint_as_float(gr.x << 16), __uint_as_float(gr.x & 0xffff0000u),
+                                   __uint_as_float(gr.y << 16), __uint_as_float(gr.y & 0xffff0000u)};
+              const float u4[4] = {__uint_as_float(ur.x << 16), __uint_as_float(ur.x & 0xffff0000u),
+                                   __uint_as_float(ur.y << 16), __uint_as_float(ur.y & 0xffff0000u)};
+              float dg[4], du[4];
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const float dh = p.alpha * acc[i][j][4 * q + v];
+                const float sg = sigmoid_f(g4[v]);
+                const float sl = g4[v] * sg;
+                const float dhp = dh * pr;
+                dg[v] = dhp * u4[v] * sg * (1.0f + g4[v] * (1.0f - sg));
+                du[v] = dhp * sl;
+                if (fin) rs[i] += dh * sl * u4[v];
+              }
+              const int unit = (wn * WTN + j * 32) / 4 + 2 * q + lk;
+              stage_unit(lr, unit, pack4(dg[0], dg[1], dg[2], dg[3]));
+              stage_unit(RG + lr, unit, pack4(du[0], du[1], du[2], du[3]));
             }
-            du_pk[i][j][q] = pack4(du[0], du[1], du[2], du[3]);
-            stage_unit(row, (wn * WTN + j * 32) / 4 + 2 * q + lk, pack4(dg[0], dg[1], dg[2], dg[3]));
-          }
-        rs[i] += __shfl_xor(rs[i], 32, kWave);  // lanes l and l+32 share the row
+          rs[i] += __shfl_xor(rs[i], 32, kWave);  // lanes l and l+32 share the row
+        }
+        barrier_nofence();
+        // dg -> dy1[:, f], du -> dy1[:, F + f] for the group's rows
+        for (int idx = tid; idx < 2 * RG * (BN / 8); idx += NT) {
+          const int region = idx / (RG * (BN / 8));
+          const int rem = idx - region * (RG * (BN / 8));
+          const int lr = rem / (BN / 8), ch = rem - lr * (BN / 8);
+          const int row = (lr / WRG) * WTM + h * WRG + (lr % WRG);
+          const int m = m0 + row, f = nt * BN + ch * 8;
+          if (m < m_end && f < F)
+            *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + region * F + f) = load_chunk(region * RG + lr, ch);
+        }
+        if (h + 1 < EPI2_NH) barrier_nofence();  // the next group reuses the regions
       }
       if (lk == 0) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) sRed[wn * BM + wm * WTM + i * 32 + lrow] = rs[i];
       }
       barrier_nofence();
-      // dg -> dy1[:, f]
-      for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
-        const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
-        const int m = m0 + row, f = nt * BN + ch * 8;
-        if (m < m_end && f < F) *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + f) = load_chunk(row, ch);
-      }
       // dp partial sums per 128-column group (independent of the tile width)
       constexpr int WPG = 128 / WTN;                    // waves per 128-column group
       constexpr int NGRP = (WN / WPG) > 0 ? (WN / WPG) : 1;
@@ -827,24 +855,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         const int gcol = nt * BN + grp * 128;
         if (m < m_end && gcol < F) p.dp_part[(int64_t)(gcol >> 7) * p.M + m] = s;
       }
-      barrier_nofence();
-      // du -> dy1[:, F + f]
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            stage_unit(wm * WTM + i * 32 + lrow, (wn * WTN + j * 32) / 4 + 2 * q + lk, du_pk[i][j][q]);
-      barrier_nofence();
-      for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
-        const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
-        const int m = m0 + row, f = nt * BN + ch * 8;
-        if (m < m_end && f < F) *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + F + f) = load_chunk(row, ch);
-      }
     }
   }
 }
+
 
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
@@ -887,7 +901,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
 // 15: 128x256 (2x4, 4)  16: 128x256 (2x4, 6)  17: 256x128 (4x2, 6)
 enum { kNumTileCfgs = 18 };
 // Defaults from a sweep of the C1 products on MI355X.
-enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 11 };
+enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 3 };
 
 template <int EPI>
 static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
