@@ -356,5 +356,18 @@ def moe_lora_layer(x, base: FrozenExperts, a_g, b_g, a_u, b_u, a_d, b_d, *, k: i
         if a_r.dim() != 2 or b_r.dim() != 2 or a_r.shape[1] != b_r.shape[0] \
                 or a_r.shape[0] != base.hidden or b_r.shape[1] != base.num_experts:
             raise ValueError("router LoRA must be A_r [H, r], B_r [r, E]")
+    if x.shape[0] == 0:
+        # No tokens: zeros that stay in the autograd graph (every LoRA factor
+        # gets a zero gradient), as the reference's empty-input paths do
+        # (runtime/bridge_runtime.py:812-823, lora.py:831-832).
+        zero = x.sum() * 0.0
+        for p in (a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r):
+            if p is not None:
+                zero = zero + p.sum().to(x.dtype) * 0.0
+        y = zero.expand(0, x.shape[1]).clone()
+        idx = torch.zeros((0, k), dtype=torch.int32, device=x.device)
+        counts = torch.zeros(base.num_experts, dtype=torch.int32, device=x.device)
+        status = torch.zeros(1, dtype=torch.int32, device=x.device)
+        return y, idx, counts, status
     return _MoELoRALayerFn.apply(x, logits, target, a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, base,
                                  k, scales, float(scale_r), bool(fuse_main_grad))

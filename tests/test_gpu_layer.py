@@ -93,6 +93,25 @@ def test_layer_c0_given_logits(device):
     _compare(got, ref, ["y", "dx", "dlogits"] + ["d" + n for n in NAMES])
 
 
+def test_layer_zero_tokens(device):
+    """T = 0: the fused layer returns [0, H] outputs that stay in the autograd
+    graph, zero LoRA gradients of the right shapes and an empty routing."""
+    from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
+    print("layer zero tokens", flush=True)
+    inp = _small("C0", 256)
+    base = FrozenExperts.build(inp.w_r.to(device), inp.w1.to(device), inp.w2.to(device))
+    lora = [inp.lora[n].to(device).requires_grad_() for n in NAMES]
+    x = torch.zeros(0, inp.x.shape[1], dtype=torch.bfloat16, device=device, requires_grad=True)
+    s = 2.0
+    y, idx, counts, status = moe_lora_layer(x, base, *lora, k=2, scales=(s, s, s))
+    assert y.shape == (0, inp.x.shape[1]) and y.requires_grad
+    assert idx.shape[0] == 0 and int(counts.sum().item()) == 0 and int(status.item()) == 0
+    y.sum().backward()
+    assert x.grad is not None and x.grad.shape == x.shape
+    for p in lora:
+        assert p.grad is not None and p.grad.shape == p.shape and not p.grad.float().abs().any()
+
+
 def test_layer_c0_router_weights(device):
     """C0 with the router gating linear on the GPU: logits within 1e-5; the
     oracle then replays the GPU's selection (near-ties may legitimately differ)."""

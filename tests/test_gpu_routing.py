@@ -43,13 +43,15 @@ def _check_plan(plan, idx_np, e, w=None):
     assert int(plan.status.item()) == 0
 
 
-@pytest.mark.parametrize("t,e,k", [(8192, 128, 8), (256, 8, 2), (1000, 64, 6), (3, 5, 5), (130, 300, 4)])
+@pytest.mark.parametrize("t,e,k", [(8192, 128, 8), (256, 8, 2), (1000, 64, 6), (3, 5, 5), (130, 300, 4),
+                                   (500, 256, 8), (700, 1024, 32), (0, 128, 8)])
 def test_topk_softmax_bit_exact(device, t, e, k):
     ops = _ops()
     print(f"topk t={t} e={e} k={k}", flush=True)
     g = torch.Generator().manual_seed(t + e + k)
     logits = torch.randn(t, e, generator=g)
-    logits[0, : min(4, e)] = 0.5  # exact ties
+    if t:
+        logits[0, : min(4, e)] = 0.5  # exact ties
     idx, w = ops.router_topk(logits.to(device), k)
     torch.cuda.synchronize()
     exp_idx, exp_w = R.topk_softmax(logits.numpy(), k)
@@ -120,7 +122,8 @@ def test_replay_rejects_out_of_range_and_repeated_ids(device):
     assert int(plan.status.item()) == 2  # the two rejected slots again
 
 
-@pytest.mark.parametrize("t,e,k", [(8192, 128, 8), (0, 8, 2), (1, 4, 4), (64, 1, 1), (4097, 256, 8)])
+@pytest.mark.parametrize("t,e,k", [(8192, 128, 8), (0, 8, 2), (1, 4, 4), (64, 1, 1), (4097, 256, 8),
+                                   (3000, 1024, 32)])
 def test_dispatch_plan_bit_exact(device, t, e, k):
     ops = _ops()
     print(f"plan t={t} e={e} k={k}", flush=True)
