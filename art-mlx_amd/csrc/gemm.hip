@@ -972,7 +972,7 @@ static int check_common(const void *a, int64_t lda, const void *b, int64_t ldb,
   ART_REQUIRE(M >= 0 && M < INT32_MAX, "%s: M out of range", who);
   ART_REQUIRE(K > 0 && K % 16 == 0, "%s: K must be a positive multiple of 16 (K=%d)", who, K);
   ART_REQUIRE(kt >= 0 && kt % 16 == 0, "%s: LoRA kt must be a multiple of 16 (kt=%d)", who, kt);
-  ART_REQUIRE(a && b && seg, "%s: null pointer", who);
+  ART_REQUIRE((a || M == 0) && b && seg, "%s: null pointer", who);  // no rows: A is never read
   ART_REQUIRE(lda >= K && lda % 8 == 0 && ldb >= K && ldb % 8 == 0,
               "%s: leading dimensions must be >= K and multiples of 8 (lda=%lld ldb=%lld)", who,
               (long long)lda, (long long)ldb);
@@ -982,7 +982,7 @@ static int check_common(const void *a, int64_t lda, const void *b, int64_t ldb,
   ART_REQUIRE((double)M * (double)lda * 2.0 < k4g && (double)M * (double)ldt * 2.0 < k4g,
               "%s: A / Tl rows must span less than 4 GiB", who);
   if (kt) {
-    ART_REQUIRE(tl && l, "%s: kt > 0 needs tl and l", who);
+    ART_REQUIRE((tl || M == 0) && l, "%s: kt > 0 needs tl and l", who);
     ART_REQUIRE(ldt >= kt && ldt % 8 == 0 && ldl >= kt && ldl % 8 == 0,
                 "%s: LoRA leading dimensions must be >= kt and multiples of 8", who);
     ART_REQUIRE(aligned16(tl) && aligned16(l), "%s: LoRA operands must be 16-byte aligned", who);
@@ -1032,7 +1032,8 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   if (rc) return rc;
   rc = check_fp8(b_format, b, ldb, b_scale, bs_estride, K, N, lda, a_scale, "grouped_gemm");
   if (rc) return rc;
-  ART_REQUIRE(N > 0 && N % 8 == 0 && c, "grouped_gemm: need N a positive multiple of 8 and an output");
+  ART_REQUIRE(N > 0 && N % 8 == 0 && (c || M == 0),
+              "grouped_gemm: need N a positive multiple of 8 and an output");
   ART_REQUIRE(ldc >= N && ldc % 8 == 0 && aligned16(c),
               "grouped_gemm: C needs ldc >= N, ldc %% 8 == 0 and 16-byte alignment");
   ART_REQUIRE((double)N * (double)(ldb > ldl ? ldb : ldl) * 2.0 < 4294967296.0,
@@ -1066,7 +1067,7 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
   rc = check_fp8(w1_format, w1, K, w1_scale, 2 * (int64_t)F, K, 2 * F, lda, a_scale, "fc1_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 64 == 0, "fc1_swiglu: F must be a positive multiple of 64 (F=%d)", F);
-  ART_REQUIRE(row_prob && y1 && h, "fc1_swiglu: null pointer");
+  ART_REQUIRE((row_prob && y1 && h) || M == 0, "fc1_swiglu: null pointer");
   ART_REQUIRE(aligned16(y1) && aligned16(h), "fc1_swiglu: outputs must be 16-byte aligned");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
@@ -1101,7 +1102,7 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
                  a_scale, "fc2_dgrad_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 8 == 0, "fc2_dgrad_swiglu: F must be a positive multiple of 8 (F=%d)", F);
-  ART_REQUIRE(y1 && row_prob && dy1 && dp_part, "fc2_dgrad_swiglu: null pointer");
+  ART_REQUIRE((y1 && row_prob && dy1 && dp_part) || M == 0, "fc2_dgrad_swiglu: null pointer");
   ART_REQUIRE(aligned16(y1) && aligned16(dy1), "fc2_dgrad_swiglu: y1/dy1 must be 16-byte aligned");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};

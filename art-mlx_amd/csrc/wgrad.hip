@@ -430,7 +430,7 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   ART_REQUIRE(ldl % 8 == 0 && ldr % 8 == 0, "grouped_wgrad: row strides must be multiples of 8");
   ART_REQUIRE(ldl < ((int64_t)1 << 30) && ldr < ((int64_t)1 << 30),
               "grouped_wgrad: row strides must be below 2^30 elements");
-  ART_REQUIRE(lm && r && seg && out, "grouped_wgrad: null pointer");
+  ART_REQUIRE(((lm && r) || M == 0) && seg && out, "grouped_wgrad: null pointer");
   ART_REQUIRE(((uintptr_t)lm & 15) == 0 && ((uintptr_t)r & 15) == 0,
               "grouped_wgrad: operands must be 16-byte aligned");
   ART_REQUIRE(mode == ART_MOE_WGRAD_STORE || mode == ART_MOE_WGRAD_ACCUMULATE ||

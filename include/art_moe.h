@@ -21,6 +21,9 @@
  *   - Every buffer is caller-owned device memory (allocate with hipMalloc or a
  *     framework allocator); the library allocates nothing.
  *   - bf16 buffers are passed as void* holding IEEE bfloat16 (uint16 bits).
+ *   - With no rows (M == 0, T == 0) the row-indexed buffers are never touched
+ *     and may be NULL (the data pointer of an empty tensor); the grouped
+ *     weight-gradient product still writes its zero output.
  *   - `stream` is a hipStream_t passed as void* (NULL = legacy stream).  All
  *     work of one call is enqueued on that stream; calls do not synchronize.
  *   - Return value: ART_MOE_OK (0) or a negative ART_MOE_ERR_* code; a

@@ -114,3 +114,34 @@ def test_validation_errors(device):
         quack_grouped_lora(x, a, b, [4])
     with pytest.raises(ValueError, match="Unsupported dtype"):
         quack_grouped_lora(x.float(), a, b, [2, 2])
+
+
+def test_zero_rows_give_empty_outputs_and_zero_grads(device):
+    """No rows (x.shape[0] == 0, every count 0): the operators return empty
+    outputs and zero factor gradients, and the C-ABI products accept the null
+    data pointer of an empty tensor."""
+    from art_amd import ops
+    from art_amd.megatron.kernels.grouped_lora_hip import quack_grouped_lora, quack_grouped_lora_dual
+    e, h, out, r = 4, 64, 96, 8
+    g = torch.Generator().manual_seed(11)
+    x = torch.zeros(0, h, dtype=torch.bfloat16, device=device, requires_grad=True)
+    a = (torch.randn(e, h, r, generator=g) * 0.1).to(torch.bfloat16).to(device).requires_grad_()
+    b = (torch.randn(e, r, out, generator=g) * 0.1).to(torch.bfloat16).to(device).requires_grad_()
+    counts = torch.zeros(e, dtype=torch.int64)
+    y = quack_grouped_lora(x, a, b, counts, scale=2.0)
+    assert y.shape == (0, out)
+    y.backward(torch.zeros_like(y))   # the backward takes a row-major grad_out (reference contract)
+    assert x.grad.shape == x.shape
+    assert a.grad is not None and not a.grad.float().abs().any()
+    assert b.grad is not None and not b.grad.float().abs().any()
+    a2 = a.detach().clone().requires_grad_()
+    b2 = b.detach().clone().requires_grad_()
+    yd = quack_grouped_lora_dual(x, a, b, a2, b2, counts, scale_gate=2.0, scale_up=2.0)
+    assert yd.shape == (0, 2 * out)
+    # the C-ABI products themselves at M = 0
+    seg = ops.segments_from_counts(counts, e, device)
+    w = torch.randn(e, out, h, generator=g).to(torch.bfloat16).to(device)
+    assert ops.grouped_gemm(x.detach(), w, seg, e, m=0).shape == (0, out)
+    gw = ops.grouped_wgrad(x.detach(), torch.zeros(0, out, dtype=torch.bfloat16, device=device),
+                           seg, e)
+    assert gw.shape == (e, h, out) and not gw.abs().any()
