@@ -10,6 +10,8 @@ trainer to inference:
 * megatron-bridge adapter weights: one ``AdapterWeight`` per expert and base
   weight, the gate and up adapters fused into one pair (stacked ``linear_in``,
   block-diagonal ``linear_out``, rank 2r) — adapter_export.py:105-142, 339-383;
+  for the dense linears (attention projection, packed QKV, shared / dense MLP)
+  keyed adapters per base weight — adapter_export.py:236-262, 412-434;
 * the fused 2D MoE tensors of PEFT target-parameter checkpoints and vLLM's
   fused experts (``mlp.experts.[base_layer.]lora_{A,B}.weight``, experts
   stacked along the rank): expanded to per-expert tensors as the Qwen3-MoE
@@ -121,6 +123,49 @@ def grouped_moe_adapter_weights(layer_prefix: str, gate: LoRA | None, up: LoRA |
             out[f"{base}.weight{e + down._expert_offset}"] = [simple_adapter_weight(
                 base, down, expert_idx=e)]
     return out
+
+
+def _set_lora_weights(out: dict[str, list[AdapterWeight]], base_prefix: str,
+                      *items: tuple[LoRA | None, str | None]) -> None:
+    weights = [simple_adapter_weight(base_prefix, lora, adapter_key=key)
+               for lora, key in items if lora is not None]
+    if weights:
+        out[f"{base_prefix}.weight"] = weights
+
+
+def add_self_attention_adapter_weights(out: dict[str, list[AdapterWeight]], *, layer_prefix: str,
+                                       self_attention: Any) -> None:
+    """Adapters of an attention block's dense LoRA linears, added to ``out``
+    (weights/adapter_export.py:236-262): ``linear_proj`` / ``out_proj`` as one
+    plain adapter, the packed ``linear_qkv`` as keyed adapters ``adapter_q``,
+    ``adapter_k``, ``adapter_v`` (those present) under one base weight."""
+    from .dense_lora import SelfAttentionLinearProjLoRA, SelfAttentionLinearQKVLoRA
+    for attr in ("linear_proj", "out_proj"):
+        proj = getattr(self_attention, attr, None)
+        if isinstance(proj, SelfAttentionLinearProjLoRA):
+            _set_lora_weights(out, f"{layer_prefix}.self_attention.{attr}", (proj.lora, None))
+    qkv = getattr(self_attention, "linear_qkv", None)
+    if isinstance(qkv, SelfAttentionLinearQKVLoRA):
+        _set_lora_weights(out, f"{layer_prefix}.self_attention.linear_qkv",
+                          (qkv.q_proj_lora, "adapter_q"), (qkv.k_proj_lora, "adapter_k"),
+                          (qkv.v_proj_lora, "adapter_v"))
+
+
+def add_split_mlp_adapter_weights(out: dict[str, list[AdapterWeight]], base_prefix: str,
+                                  mlp: Any) -> None:
+    """Adapters of a split (gate / up / down) dense MLP, added to ``out``
+    (weights/adapter_export.py:412-434): ``linear_fc1`` as keyed adapters
+    ``adapter_gate`` and ``adapter_up``; ``linear_fc2`` as one plain adapter
+    when it is a projection-style linear.  The same type test as the
+    reference: a ``SharedExpertsLinearFC2LoRA`` wrapper does not match it."""
+    from .dense_lora import SelfAttentionLinearProjLoRA, SharedExpertsLinearFC1LoRA
+    fc1 = getattr(mlp, "linear_fc1", None)
+    if isinstance(fc1, SharedExpertsLinearFC1LoRA):
+        _set_lora_weights(out, f"{base_prefix}.linear_fc1", (fc1.gate_lora, "adapter_gate"),
+                          (fc1.up_lora, "adapter_up"))
+    fc2 = getattr(mlp, "linear_fc2", None)
+    if isinstance(fc2, SelfAttentionLinearProjLoRA):
+        _set_lora_weights(out, f"{base_prefix}.linear_fc2", (fc2.lora, None))
 
 
 def module_loras(linear_fc1: MLPExpertsLinearFC1LoRA, linear_fc2: MLPExpertsLinearFC2LoRA

@@ -220,3 +220,62 @@ def test_alpha_must_be_integral():
     lora.scale = 0.3   # alpha 0.9
     with pytest.raises(ValueError, match="integer alpha"):
         A.adapter_alpha_dim(lora)
+
+
+def _dense_modules(seed=0):
+    from art_amd.megatron.dense_lora import (SelfAttentionLinearProjLoRA, SelfAttentionLinearQKVLoRA,
+                                             SharedExpertsLinearFC1LoRA, SharedExpertsLinearFC2LoRA)
+    g = torch.Generator().manual_seed(seed)
+    qkv = SelfAttentionLinearQKVLoRA("l.self_attn", torch.zeros(2 * (32 + 32), 64, dtype=torch.bfloat16),
+                                     4, 8, num_attention_heads=4, num_query_groups=2, kv_channels=16)
+    proj = SelfAttentionLinearProjLoRA("l.self_attn.o_proj", torch.zeros(64, 64, dtype=torch.bfloat16), 4, 8)
+    fc1 = SharedExpertsLinearFC1LoRA("l.mlp", torch.zeros(96, 64, dtype=torch.bfloat16), 4, 8)
+    fc2 = SharedExpertsLinearFC2LoRA("l.mlp", torch.zeros(64, 48, dtype=torch.bfloat16), 4, 8)
+    with torch.no_grad():
+        for m in (qkv, proj, fc1, fc2):
+            for p in m.parameters():
+                p.copy_(torch.randn(p.shape, generator=g).to(p.dtype))
+    return qkv, proj, fc1, fc2
+
+
+def test_self_attention_adapter_weights_keys_and_tensors():
+    """Attention export (adapter_export.py:236-262): linear_proj plain, linear_qkv
+    as adapter_q / adapter_k / adapter_v under one base weight."""
+    from types import SimpleNamespace
+    qkv, proj, _, _ = _dense_modules()
+    out = {}
+    A.add_self_attention_adapter_weights(out, layer_prefix="decoder.layers.3",
+                                         self_attention=SimpleNamespace(linear_qkv=qkv, linear_proj=proj))
+    assert sorted(out) == ["decoder.layers.3.self_attention.linear_proj.weight",
+                           "decoder.layers.3.self_attention.linear_qkv.weight"]
+    (pw,) = out["decoder.layers.3.self_attention.linear_proj.weight"]
+    assert pw.adapter_key is None and (pw.alpha, pw.dim) == (8, 4)
+    assert pw.linear_in_name == "decoder.layers.3.self_attention.linear_proj.adapter.linear_in.weight"
+    assert torch.equal(pw.linear_in, proj.lora.A_T.detach().t())
+    assert torch.equal(pw.linear_out, proj.lora.B_T.detach().t())
+    ws = out["decoder.layers.3.self_attention.linear_qkv.weight"]
+    assert [w.adapter_key for w in ws] == ["adapter_q", "adapter_k", "adapter_v"]
+    assert ws[1].linear_out_name.endswith("linear_qkv.adapter.adapter_k.linear_out.weight")
+    for w, lora in zip(ws, (qkv.q_proj_lora, qkv.k_proj_lora, qkv.v_proj_lora)):
+        assert torch.equal(w.linear_out, lora.B_T.detach().t())
+    assert ws[0].linear_out.shape == (2 * 32, 4) and ws[2].linear_out.shape == (2 * 16, 4)
+
+
+def test_split_mlp_adapter_weights_match_reference_type_rules():
+    """Dense MLP export (adapter_export.py:412-434): gate / up keyed adapters on
+    linear_fc1; linear_fc2 only when it is a projection-style linear, so the
+    shared-expert FC2 wrapper is skipped exactly as in the reference."""
+    from types import SimpleNamespace
+    _, proj, fc1, fc2 = _dense_modules(1)
+    out = {}
+    A.add_split_mlp_adapter_weights(out, "decoder.layers.0.mlp.shared_experts",
+                                    SimpleNamespace(linear_fc1=fc1, linear_fc2=fc2))
+    assert list(out) == ["decoder.layers.0.mlp.shared_experts.linear_fc1.weight"]
+    gate, up = out["decoder.layers.0.mlp.shared_experts.linear_fc1.weight"]
+    assert (gate.adapter_key, up.adapter_key) == ("adapter_gate", "adapter_up")
+    assert torch.equal(up.linear_in, fc1.up_lora.A_T.detach().t())
+    out = {}
+    A.add_split_mlp_adapter_weights(out, "decoder.layers.0.mlp",
+                                    SimpleNamespace(linear_fc1=fc1, linear_fc2=proj))
+    (w2,) = out["decoder.layers.0.mlp.linear_fc2.weight"]
+    assert w2.adapter_key is None and torch.equal(w2.linear_out, proj.lora.B_T.detach().t())
