@@ -58,15 +58,22 @@ _SEGS: dict = {}
 
 def _segments(t: int, pieces: int, device) -> torch.Tensor:
     """Segment table of ``t`` rows cut into ``pieces`` near-equal segments
-    (cached: a handful of (t, pieces) pairs recur every step)."""
+    (cached: a handful of (t, pieces) pairs recur every step).
+
+    A new table is built on the current stream and the stream is synchronised
+    once, so a cached table is complete whichever stream reads it later.
+    Nothing is cached while a stream is being captured into a graph."""
     key = (t, pieces, str(device))
     seg = _SEGS.get(key)
     if seg is None:
+        base, extra = divmod(t, pieces)
+        seg = ops.segments_from_counts([base + (i < extra) for i in range(pieces)], pieces, device)
+        if torch.cuda.is_current_stream_capturing():
+            return seg
+        torch.cuda.current_stream(seg.device).synchronize()
         if len(_SEGS) > 64:
             _SEGS.clear()
-        base, extra = divmod(t, pieces)
-        seg = _SEGS[key] = ops.segments_from_counts(
-            [base + (i < extra) for i in range(pieces)], pieces, device)
+        _SEGS[key] = seg
     return seg
 
 
