@@ -30,10 +30,20 @@ B_BF16 = 0
 B_FP8_ROWSCALE = 1
 B_FP8_KSCALE = 2
 AB_FP8 = 3
+F16 = 4
+WGRAD_F16 = 16
 
 
 def seg_len(num_experts: int) -> int:
     return (1 + SEG_NBM) * (num_experts + 1)
+
+
+def experts_of_seg(seg) -> int:
+    """Number of experts E of a segment table of seg_len(E) entries."""
+    n = seg.numel()
+    if n % (1 + SEG_NBM) or n < 2 * (1 + SEG_NBM):
+        raise ValueError(f"{n} entries is not a segment table length")
+    return n // (1 + SEG_NBM) - 1
 
 
 _P = ctypes.c_void_p
@@ -69,6 +79,7 @@ SIGNATURES = {
     "art_moe_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
     "art_moe_pack": (_I32, [_P, _I32, _P]),
+    "art_moe_pack_typed": (_I32, [_P, _I32, _I32, _P]),
     "art_moe_weighted_swiglu": (_I32, [_P, _P, _I64, _I32, _P, _P]),
     "art_moe_weighted_swiglu_back": (_I32, [_P, _P, _P, _I64, _I32, _P, _P, _P]),
     "art_moe_router_lora_apply": (_I32, [_P, _I64, _I32, _P, _I32, _F, _P, _P, _P]),

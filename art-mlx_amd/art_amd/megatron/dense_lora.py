@@ -54,26 +54,35 @@ class Placement:
 
 
 _SEGS: dict = {}
+_SEGS_MAX = 64
 
 
 def _segments(t: int, pieces: int, device) -> torch.Tensor:
-    """Segment table of ``t`` rows cut into ``pieces`` near-equal segments
-    (cached: a handful of (t, pieces) pairs recur every step).
+    """Segment table of ``t`` rows cut into ``pieces`` near-equal segments.
 
-    A new table is built on the current stream and the stream is synchronised
-    once, so a cached table is complete whichever stream reads it later.
-    Nothing is cached while a stream is being captured into a graph."""
+    The counts are filled on the device (no host copy, so this also works
+    while a stream is captured into a graph).  Outside capture the table is
+    cached per (t, pieces, device) with an event recorded after it was built;
+    a later caller on any stream waits on that event on the device before
+    reading it.  Cached tables are never dropped (the cache stops growing at
+    _SEGS_MAX keys and later keys are built per call), so no stream can still
+    be reading memory the allocator has handed out again."""
     key = (t, pieces, str(device))
-    seg = _SEGS.get(key)
-    if seg is None:
-        base, extra = divmod(t, pieces)
-        seg = ops.segments_from_counts([base + (i < extra) for i in range(pieces)], pieces, device)
-        if torch.cuda.is_current_stream_capturing():
-            return seg
-        torch.cuda.current_stream(seg.device).synchronize()
-        if len(_SEGS) > 64:
-            _SEGS.clear()
-        _SEGS[key] = seg
+    capturing = torch.cuda.is_current_stream_capturing()
+    hit = None if capturing else _SEGS.get(key)
+    if hit is not None:
+        seg, ready = hit
+        torch.cuda.current_stream(seg.device).wait_event(ready)
+        return seg
+    base, extra = divmod(t, pieces)
+    counts = torch.full((pieces,), base, dtype=torch.int64, device=device)
+    if extra:
+        counts[:extra] += 1
+    seg = ops.segments_from_counts(counts, pieces, device)
+    if not capturing and len(_SEGS) < _SEGS_MAX:
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(seg.device))
+        _SEGS[key] = (seg, ready)
     return seg
 
 

@@ -72,13 +72,28 @@ def _validate_inputs(x, a_t, b_t, tokens_per_expert) -> torch.Tensor:
             f"got {counts.numel()} and {a_t.shape[0]}")
     if x.device.type != "cuda" or a_t.device != x.device or b_t.device != x.device:
         raise ValueError("x, a_t, and b_t must be CUDA tensors on the same device")
-    if x.dtype != torch.bfloat16:
-        raise ValueError(f"Unsupported dtype {x.dtype}; expected bf16")
+    if x.dtype not in {torch.float16, torch.bfloat16}:
+        raise ValueError(f"Unsupported dtype {x.dtype}; expected fp16 or bf16")
     if a_t.dtype != x.dtype or b_t.dtype != x.dtype:
         raise ValueError(f"Dtype mismatch: x={x.dtype}, a_t={a_t.dtype}, b_t={b_t.dtype}")
     if x.shape[1] % 8 or b_t.shape[-1] % 8:
         raise ValueError("in_features and out_features must be multiples of 8")
+    _check_rows(counts, x)
     return counts
+
+
+def _check_rows(counts: torch.Tensor, x: torch.Tensor) -> None:
+    """sum(counts) <= x.shape[0] when the counts are on the host (no sync).
+
+    The reference leaves ``sum(counts) == x.shape[0]`` to the caller
+    (cute_grouped_lora_quack.py:642-651).  Host counts cost nothing to check;
+    device counts are not read back, and the kernels clamp every segment to
+    the rows of x instead."""
+    if counts.device.type == "cpu":
+        total = int(counts.sum())
+        if total > x.shape[0]:
+            raise ValueError(
+                f"tokens_per_expert sums to {total}, more than the {x.shape[0]} rows of x")
 
 
 def _validate_dual_inputs(x, gate_a_t, gate_b_t, up_a_t, up_b_t, tokens_per_expert):
@@ -252,7 +267,7 @@ def quack_grouped_lora(x, a_t, b_t, counts, scale: float = 1.0) -> torch.Tensor:
 
     Caller contract (as in the reference): ``counts`` ordered by local expert,
     ``sum(counts) == x.shape[0]`` (not checked: no host sync), ``x`` 2-D,
-    ``a_t [E, in, r]``, ``b_t [E, r, out]``, same CUDA device, bf16.
+    ``a_t [E, in, r]``, ``b_t [E, r, out]``, same CUDA device, fp16 or bf16.
     """
     counts_tensor = _validate_inputs(x, a_t, b_t, counts)
     return _HipGroupedLoraFn.apply(x, a_t, b_t, counts_tensor, scale)

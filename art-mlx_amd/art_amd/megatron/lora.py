@@ -20,13 +20,30 @@ expert path:
   tests/integration/megatron/routing_replay/trace.py:498-513): FC1 LoRA ->
   weighted SwiGLU -> FC2 LoRA.
 
-Not mirrored: multi-adapter slots (``LoRASlotRef``), tensor-parallel sharding
-metadata and adapter loading from PEFT checkpoints.  The fused, faster path
-for the whole layer is ``moe_layer.moe_lora_layer``.
+* Adapter slots (lora.py:59-85, 422-449, 549-600, 804-835): a ``LoRA`` can
+  hold extra named adapters (``LoRASlotRef(kind, name)`` -> ``LoRASlot`` with
+  its own ``A_T``/``B_T``, rank and ``scale = alpha / rank``), loaded from a
+  PEFT-keyed adapter dict with ``load_lora_slot``.  ``use_lora_slot(ref)``
+  selects one for the forwards run inside it; ``active_lora_tensors`` returns
+  the selected factors, or None for a base-model ref (name None) or a slot
+  this module does not hold, and the forward then returns zeros.  The gate/up
+  dual product falls back to the two single adapters when either is inactive
+  (lora.py:1062-1070).
+* ``MLPExpertsLinearFC1LoRA(fused_gate_up=True)`` (lora.py:1472-1497,
+  1521-1527): one ``gate_up_proj`` adapter, ``A_T [E, in, r]`` shared by gate
+  and up, ``B_T [E, r, 2F]``.
+
+Not mirrored: tensor-parallel sharding metadata (one GPU).  The fused, faster
+path for the whole layer is ``moe_layer.moe_lora_layer``.
 """
 from __future__ import annotations
 
+import contextvars
+import functools
 import math
+from contextlib import contextmanager
+from dataclasses import dataclass
+from typing import Iterator
 
 import torch
 
@@ -41,6 +58,64 @@ def _counts(tokens_per_expert) -> torch.Tensor:
     if isinstance(tokens_per_expert, list):
         return torch.tensor(tokens_per_expert, dtype=torch.int64, device="cpu")
     return tokens_per_expert
+
+
+@dataclass(frozen=True)
+class LoRASlotRef:
+    """Names an adapter slot: ``kind`` "checkpoint" or "lora"; ``name`` None
+    means the base model (no adapter) (lora.py:59-62)."""
+    kind: str
+    name: str | None
+
+
+# The slot selected for the forwards on this thread / task (None: the
+# module's own A_T, B_T).
+_ACTIVE_SLOT: contextvars.ContextVar[LoRASlotRef | None] = contextvars.ContextVar(
+    "art_amd_active_lora_slot", default=None)
+
+
+@contextmanager
+def use_lora_slot(ref: LoRASlotRef | None) -> Iterator[None]:
+    """Select ``ref`` for every LoRA forward inside the block (lora.py:69-75)."""
+    token = _ACTIVE_SLOT.set(ref)
+    try:
+        yield
+    finally:
+        _ACTIVE_SLOT.reset(token)
+
+
+def with_captured_lora_slot(function):
+    """``function`` bound to the slot selected now, so a later call (an
+    activation-checkpoint recompute in the backward) sees the same adapter
+    (lora.py:78-89)."""
+    captured = _ACTIVE_SLOT.get()
+
+    @functools.wraps(function)
+    def run(*args, **kwargs):
+        with use_lora_slot(captured):
+            return function(*args, **kwargs)
+
+    return run
+
+
+class LoRASlot(torch.nn.Module):
+    """One loaded adapter of a ``LoRA``: its own factors and scale (lora.py:422-449)."""
+
+    def __init__(self, *, ref: LoRASlotRef, a_t: torch.Tensor, b_t: torch.Tensor, alpha: float,
+                 requires_grad: bool) -> None:
+        super().__init__()
+        self.ref = ref
+        self.alpha = float(alpha)
+        self.A_T = torch.nn.Parameter(a_t.detach().clone(), requires_grad=requires_grad)
+        self.B_T = torch.nn.Parameter(b_t.detach().clone(), requires_grad=requires_grad)
+
+    @property
+    def rank(self) -> int:
+        return int(self.A_T.shape[-1])
+
+    @property
+    def scale(self) -> float:
+        return self.alpha / self.rank
 
 
 class LoRA(torch.nn.Module):
@@ -60,6 +135,8 @@ class LoRA(torch.nn.Module):
             torch.zeros(num_local_experts, in_features, rank, dtype=dtype, device=device).squeeze(0))
         self.B_T = torch.nn.Parameter(
             torch.zeros(num_local_experts, rank, out_features, dtype=dtype, device=device).squeeze(0))
+        self._slot_modules = torch.nn.ModuleDict()
+        self._slot_names: dict[LoRASlotRef, str] = {}
         self.reset_lora_parameters()
 
     @property
@@ -76,29 +153,97 @@ class LoRA(torch.nn.Module):
                 torch.nn.init.kaiming_uniform_(self.A_T.T, a=math.sqrt(5))
             self.B_T.zero_()
 
+    # ------------------------------------------------------------ slots
+    def _slot(self, ref: LoRASlotRef) -> LoRASlot | None:
+        name = self._slot_names.get(ref)
+        return None if name is None else self._slot_modules[name]
+
+    def lora_slot_params(self, ref: LoRASlotRef) -> list[torch.nn.Parameter]:
+        slot = self._slot(ref)
+        return [] if slot is None else [slot.A_T, slot.B_T]
+
+    def _factor_from_adapter(self, adapter_model: dict[str, torch.Tensor], suffix: str,
+                             like: torch.Tensor) -> torch.Tensor:
+        """A_T / B_T layout of the PEFT tensors ``<key>.<suffix>.weight`` (one
+        per expert, transposed), on this module's device and dtype."""
+        experts = range(self.num_local_experts) if self.A_T.ndim == 3 else [None]
+        mats = [adapter_model[self._keys(e, f"{suffix}.weight")].T for e in experts]
+        w = torch.stack(mats) if self.A_T.ndim == 3 else mats[0]
+        return w.to(device=like.device, dtype=like.dtype).contiguous()
+
+    def load_lora_slot(self, ref: LoRASlotRef, adapter_model: dict[str, torch.Tensor], *,
+                       alpha: float = LORA_ALPHA, requires_grad: bool) -> bool:
+        """Load this module's part of ``adapter_model`` into slot ``ref``.
+
+        False when the adapter has none of this module's keys; KeyError when it
+        has only some; RuntimeError when the slot exists and still holds
+        gradients (lora.py:549-581).  The slot's rank is the adapter's."""
+        if ref.name is None:
+            raise ValueError("base-model slot refs do not own LoRA tensors")
+        experts = range(self.num_local_experts) if self.A_T.ndim == 3 else [None]
+        keys = [self._keys(e, f"{suffix}.weight") for suffix in ("lora_A", "lora_B")
+                for e in experts]
+        absent = sorted(k for k in keys if k not in adapter_model)
+        if len(absent) == len(keys):
+            return False
+        if absent:
+            raise KeyError(f"Incomplete LoRA adapter keys for {self.adapter_model_prefix}: {absent}")
+        a_t = self._factor_from_adapter(adapter_model, "lora_A", self.A_T)
+        b_t = self._factor_from_adapter(adapter_model, "lora_B", self.B_T)
+        old = self._slot(ref)
+        if old is not None and any(p.grad is not None for p in (old.A_T, old.B_T)):
+            raise RuntimeError(
+                f"Cannot overwrite live LoRA slot {ref.kind}:{ref.name} for "
+                f"{self.adapter_model_prefix}; clear grads/backward graph first.")
+        name = self._slot_names.setdefault(ref, f"slot_{len(self._slot_names)}")
+        self._slot_modules[name] = LoRASlot(ref=ref, a_t=a_t, b_t=b_t, alpha=alpha,
+                                            requires_grad=requires_grad)
+        return True
+
+    def active_lora_tensors(self) -> tuple[torch.Tensor, torch.Tensor, float] | None:
+        """(A_T, B_T, scale) of the selected slot (lora.py:804-815): the module's
+        own without a selection, None for a base-model ref or a slot it lacks."""
+        ref = _ACTIVE_SLOT.get()
+        if ref is None:
+            return self.A_T, self.B_T, self.scale
+        if ref.name is None:
+            return None
+        slot = self._slot(ref)
+        return None if slot is None else (slot.A_T, slot.B_T, slot.scale)
+
     def forward(self, x: torch.Tensor, tokens_per_expert=None) -> torch.Tensor:
+        active = self.active_lora_tensors()
+        if active is None:   # no adapter selected for this module: no contribution
+            return x.new_zeros((*x.shape[:-1], self.out_features))
+        a_t, b_t, scale = active
         if tokens_per_expert is not None:
             if self.num_local_experts <= 1:
                 raise ValueError("tokens_per_expert is only supported if num_local_experts > 1")
             if x.shape[0] == 0:
                 return x.new_zeros((*x.shape[:-1], self.out_features))
-            return quack_grouped_lora(x, self.A_T, self.B_T, _counts(tokens_per_expert),
-                                      scale=self.scale)
-        out = (x @ self.A_T) @ self.B_T
-        return out if self.scale == 1.0 else out * self.scale
+            return quack_grouped_lora(x, a_t, b_t, _counts(tokens_per_expert), scale=scale)
+        out = (x @ a_t) @ b_t
+        return out if scale == 1.0 else out * scale
 
     def _keys(self, expert: int | None, suffix: str) -> str:
         if expert is None:
             return f"{self.adapter_model_prefix}.{suffix}"
         return f"{self.adapter_model_prefix.format(expert=expert + self._expert_offset)}.{suffix}"
 
-    def sharded_lora_state_dict(self) -> dict[str, torch.Tensor]:
-        """PEFT layout: lora_A.weight = A_T[e].T [r, in], lora_B.weight = B_T[e].T [out, r]."""
+    def sharded_lora_state_dict(self, ref: LoRASlotRef | None = None) -> dict[str, torch.Tensor]:
+        """PEFT layout: lora_A.weight = A_T[e].T [r, in], lora_B.weight = B_T[e].T [out, r]
+        (of slot ``ref`` when given; empty if this module lacks it)."""
         out: dict[str, torch.Tensor] = {}
+        a_t, b_t = self.A_T, self.B_T
+        if ref is not None:
+            slot = self._slot(ref)
+            if slot is None:
+                return out
+            a_t, b_t = slot.A_T, slot.B_T
         experts = range(self.num_local_experts) if self.A_T.ndim == 3 else [None]
         for e in experts:
-            a = self.A_T.data[e] if e is not None else self.A_T.data
-            b = self.B_T.data[e] if e is not None else self.B_T.data
+            a = a_t.data[e] if e is not None else a_t.data
+            b = b_t.data[e] if e is not None else b_t.data
             out[self._keys(e, "lora_A.weight")] = a.T
             out[self._keys(e, "lora_B.weight")] = b.T
         return out
@@ -154,28 +299,47 @@ class GroupedLinear(torch.nn.Module):
 
 
 class MLPExpertsLinearFC1LoRA(torch.nn.Module):
+    """Frozen grouped FC1 plus either separate gate / up adapters (a shared
+    projection through the dual product) or, with ``fused_gate_up``, one
+    ``gate_up_proj`` adapter whose B covers both halves (lora.py:1464-1529)."""
+
     def __init__(self, adapter_model_prefix: str, linear_fc1: GroupedLinear, rank: int,
-                 alpha: float, num_local_experts: int) -> None:
+                 alpha: float, num_local_experts: int, fused_gate_up: bool = False) -> None:
         super().__init__()
         self.linear_fc1 = linear_fc1
+        self.fused_gate_up = bool(fused_gate_up)
         f = linear_fc1.out_features // 2
         w = linear_fc1.weight
         dtype = torch.bfloat16 if w.dtype != torch.float32 else w.dtype
         kw = dict(rank=rank, alpha=alpha, dtype=dtype, device=w.device,
                   num_local_experts=num_local_experts)
-        self.gate_lora = LoRA(f"{adapter_model_prefix}.{{expert}}.gate_proj",
-                              linear_fc1.in_features, f, **kw)
-        self.up_lora = LoRA(f"{adapter_model_prefix}.{{expert}}.up_proj",
-                            linear_fc1.in_features, f, **kw)
+        if self.fused_gate_up:
+            self.lora = LoRA(f"{adapter_model_prefix}.{{expert}}.gate_up_proj",
+                             linear_fc1.in_features, linear_fc1.out_features, **kw)
+        else:
+            self.gate_lora = LoRA(f"{adapter_model_prefix}.{{expert}}.gate_proj",
+                                  linear_fc1.in_features, f, **kw)
+            self.up_lora = LoRA(f"{adapter_model_prefix}.{{expert}}.up_proj",
+                                linear_fc1.in_features, f, **kw)
+
+    def _dual(self, x: torch.Tensor, tokens_per_expert) -> torch.Tensor:
+        gate = self.gate_lora.active_lora_tensors()
+        up = self.up_lora.active_lora_tensors()
+        if gate is None or up is None:   # one side inactive: the two singles (lora.py:1062-1070)
+            return torch.cat([self.gate_lora(x, tokens_per_expert=tokens_per_expert),
+                              self.up_lora(x, tokens_per_expert=tokens_per_expert)], dim=-1)
+        (ga, gb, gs), (ua, ub, us) = gate, up
+        return quack_grouped_lora_dual(x, ga, gb, ua, ub, _counts(tokens_per_expert),
+                                       scale_gate=gs, scale_up=us)
 
     def forward(self, x: torch.Tensor, tokens_per_expert):
         base, bias = self.linear_fc1(x, tokens_per_expert)
         if x.shape[0] == 0:
             return base, bias
-        adapter = quack_grouped_lora_dual(
-            x, self.gate_lora.A_T, self.gate_lora.B_T, self.up_lora.A_T, self.up_lora.B_T,
-            _counts(tokens_per_expert), scale_gate=self.gate_lora.scale,
-            scale_up=self.up_lora.scale)
+        if self.fused_gate_up:
+            adapter = self.lora(x, tokens_per_expert=tokens_per_expert)
+        else:
+            adapter = self._dual(x, tokens_per_expert)
         return base + adapter, bias
 
 

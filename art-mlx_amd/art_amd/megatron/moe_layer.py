@@ -186,24 +186,30 @@ class _MoELoRALayerFn(torch.autograd.Function):
         t = x.shape[0]
         logits_supplied = logits is not None
         seg1 = _single_segment(t, x.device)
-        rg, ru, rd = a_g.shape[-1], a_u.shape[-1], a_d.shape[-1]
-        rpg, rpu, rpd = padded_rank(rg), padded_rank(ru), padded_rank(rd)
+        # FC1 adapter: gate and up (separate A, a shared projection) or, with
+        # a_u = b_u = None, one gate|up adapter (A shared, B over both halves).
+        fused_gu = a_u is None
+        rg, rd = a_g.shape[-1], a_d.shape[-1]
+        ru = 0 if fused_gu else a_u.shape[-1]
+        rpg, rpu, rpd = padded_rank(rg), (padded_rank(ru) if ru else 0), padded_rank(rd)
         rr = a_r.shape[-1] if a_r is not None else 0
         rpr = padded_rank(rr) if rr else 0
         # LoRA operand layouts, rebuilt every call since the factors train: one
         # launch writes the transposed, rank-padded and scaled copies
-        a1p = x.new_empty((e, rpg + rpu, h_dim))   # [A_g | A_u]^T
-        l1 = x.new_empty((e, 2 * f, rpg + rpu))    # [[s_g B_g^T, 0], [0, s_u B_u^T]]
+        a1p = x.new_empty((e, rpg + rpu, h_dim))   # [A_g | A_u]^T  (fused: A^T)
+        l1 = x.new_empty((e, 2 * f, rpg + rpu))    # [[s_g B_g^T, 0], [0, s_u B_u^T]]  (fused: s B^T)
         a2p = x.new_empty((e, rpd, f))             # A_d^T
         l2 = x.new_empty((e, h_dim, rpd))          # s_d B_d^T
-        items = [(a1p[:, :rpg], a_g.transpose(1, 2), 1.0),
-                 (a1p[:, rpg:], a_u.transpose(1, 2), 1.0),
-                 (l1[:, :f, :rpg], b_g.transpose(1, 2), sg),
-                 (l1[:, :f, rpg:], None, 0.0),
-                 (l1[:, f:, :rpg], None, 0.0),
-                 (l1[:, f:, rpg:], b_u.transpose(1, 2), su),
-                 (a2p, a_d.transpose(1, 2), 1.0),
-                 (l2, b_d.transpose(1, 2), sd)]
+        if fused_gu:
+            items = [(a1p, a_g.transpose(1, 2), 1.0), (l1, b_g.transpose(1, 2), sg)]
+        else:
+            items = [(a1p[:, :rpg], a_g.transpose(1, 2), 1.0),
+                     (a1p[:, rpg:], a_u.transpose(1, 2), 1.0),
+                     (l1[:, :f, :rpg], b_g.transpose(1, 2), sg),
+                     (l1[:, :f, rpg:], None, 0.0),
+                     (l1[:, f:, :rpg], None, 0.0),
+                     (l1[:, f:, rpg:], b_u.transpose(1, 2), su)]
+        items += [(a2p, a_d.transpose(1, 2), 1.0), (l2, b_d.transpose(1, 2), sd)]
         arp = brp = None
         if rr:
             arp = x.new_empty((1, rpr, h_dim))     # A_r^T
@@ -221,7 +227,12 @@ class _MoELoRALayerFn(torch.autograd.Function):
             status = None
         else:
             idx, w, status = ops.router_replay(logits, target)
-        plan = ops.dispatch_plan(idx, w, e, status=status)
+        # The plan counts ids < 0 as rejected; after a replay those are the ids
+        # the replay already counted, so the plan keeps its own counter and the
+        # layer reports the replay's.
+        plan = ops.dispatch_plan(idx, w, e)
+        if status is None:
+            status = plan.status
         m = t * k
         rows = plan.row_token
         t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
@@ -234,7 +245,7 @@ class _MoELoRALayerFn(torch.autograd.Function):
                                    tl=t1, l1=l1, w1_scale=base.w1_scale)
         t2 = ops.grouped_gemm(h, a2p, plan.seg, e, m=m)
         if base.act_fp8:
-            hq, hs = ops.quantize_rows_fp8(h)
+            hq, hs = ops.quantize_rows_fp8(h, seg=plan.seg)
             y2 = ops.grouped_gemm(hq, base.w2, plan.seg, e, m=m, tl=t2, l=l2,
                                   b_scale=base.w2_scale, a_scale=hs)
         else:
@@ -243,18 +254,18 @@ class _MoELoRALayerFn(torch.autograd.Function):
         ctx.save_for_backward(x, idx, w, plan.dest, rows, plan.row_prob, plan.seg, t1, y1, h, t2,
                               a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, brp, t_rb, seg1)
         ctx.base = base
-        ctx.meta = (k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd, rr, rpr, scale_r)
+        ctx.meta = (k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd, rr, rpr, scale_r, fused_gu)
         ctx.logits_supplied = logits_supplied
         ctx.fuse_main_grad = fuse_main_grad
-        ctx.mark_non_differentiable(idx, plan.counts, plan.status)
-        return y, idx, plan.counts, plan.status
+        ctx.mark_non_differentiable(idx, plan.counts, status)
+        return y, idx, plan.counts, status
 
     @staticmethod
     def backward(ctx, dy, *unused: Any):
         (x, idx, w, dest, rows, row_prob, seg, t1, y1, h, t2,
          a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r, brp, t_rb, seg1) = ctx.saved_tensors
         base: FrozenExperts = ctx.base
-        k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd, rr, rpr, scale_r = ctx.meta
+        k, sg, su, sd, rg, ru, rd, rpg, rpu, rpd, rr, rpr, scale_r, fused_gu = ctx.meta
         e, f = base.num_experts, base.ffn
         t = x.shape[0]
         m = t * k
@@ -267,9 +278,12 @@ class _MoELoRALayerFn(torch.autograd.Function):
         adp = a_d if rd == rpd and a_d.is_contiguous() else dy.new_empty((e, f, rpd))
         gb = dy.new_empty((e, rpg + rpu, 2 * f))
         a1cat = dy.new_empty((e, h_dim, rpg + rpu))
-        items = [(gb[:, :rpg, :f], b_g, sg), (gb[:, :rpg, f:], None, 0.0),
-                 (gb[:, rpg:, :f], None, 0.0), (gb[:, rpg:, f:], b_u, su),
-                 (a1cat[:, :, :rpg], a_g, 1.0), (a1cat[:, :, rpg:], a_u, 1.0)]
+        if fused_gu:   # g1 = s dy1 B^T, dx += g1 A^T
+            items = [(gb, b_g, sg), (a1cat, a_g, 1.0)]
+        else:
+            items = [(gb[:, :rpg, :f], b_g, sg), (gb[:, :rpg, f:], None, 0.0),
+                     (gb[:, rpg:, :f], None, 0.0), (gb[:, rpg:, f:], b_u, su),
+                     (a1cat[:, :, :rpg], a_g, 1.0), (a1cat[:, :, rpg:], a_u, 1.0)]
         if bdp is not b_d:
             items.append((bdp, b_d, 1.0))
         if adp is not a_d:
@@ -317,12 +331,18 @@ class _MoELoRALayerFn(torch.autograd.Function):
             dx = ops.combine(dx_perm, dest, t)
         # LoRA weight gradients: fp32 accumulation, landed in fp32 main_grad or
         # rounded once to the parameter dtype
-        gag, gau = _land_wgrad(x, g1, seg, e, [(a_g, 0), (a_u, rpg)], l_rows=rows,
-                               fuse_main_grad=fuse)
-        (gbg,) = _land_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, [(b_g, 0)], alpha=sg,
-                             transpose_out=True, fuse_main_grad=fuse)
-        (gbu,) = _land_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, [(b_u, 0)], alpha=su,
-                             transpose_out=True, fuse_main_grad=fuse)
+        if fused_gu:   # dA = x^T g1, dB = s t1^T dy1 over both halves
+            (gag,) = _land_wgrad(x, g1, seg, e, [(a_g, 0)], l_rows=rows, fuse_main_grad=fuse)
+            (gbg,) = _land_wgrad(dy1, t1, seg, e, [(b_g, 0)], alpha=sg, transpose_out=True,
+                                 fuse_main_grad=fuse)
+            gau = gbu = None
+        else:
+            gag, gau = _land_wgrad(x, g1, seg, e, [(a_g, 0), (a_u, rpg)], l_rows=rows,
+                                   fuse_main_grad=fuse)
+            (gbg,) = _land_wgrad(dy1[:, :f], t1[:, :rpg], seg, e, [(b_g, 0)], alpha=sg,
+                                 transpose_out=True, fuse_main_grad=fuse)
+            (gbu,) = _land_wgrad(dy1[:, f:], t1[:, rpg:], seg, e, [(b_u, 0)], alpha=su,
+                                 transpose_out=True, fuse_main_grad=fuse)
         (gad,) = _land_wgrad(h, g2, seg, e, [(a_d, 0)], fuse_main_grad=fuse)
         (gbd,) = _land_wgrad(dy, t2, seg, e, [(b_d, 0)], alpha=sd, l_rows=rows,
                              transpose_out=True, fuse_main_grad=fuse)
@@ -337,6 +357,11 @@ def moe_lora_layer(x, base: FrozenExperts, a_g, b_g, a_u, b_u, a_d, b_d, *, k: i
                    fuse_main_grad: bool = False):
     """Functional layer.  Returns (y [T,H] bf16, idx [T,k], counts [E], status [1]).
 
+    FC1's adapter is ``a_g [E,H,r_g], b_g [E,r_g,F]`` (gate) with ``a_u, b_u``
+    (up), or, with ``a_u = b_u = None``, one gate|up adapter ``a_g [E,H,r],
+    b_g [E,r,2F]`` whose A is shared by both halves (megatron's
+    ``fused_gate_up``, lora.py:1472-1497) at scale ``scales[0]``.
+
     ``logits`` (fp32 [T,E]) replaces the router gating linear; ``target``
     (int [T,k]) replays routes.  ``status`` counts rejected replay ids.
     ``router_lora = (A_r [H,r], B_r [r,E], scale)`` adds s (x A_r) B_r to the
@@ -347,6 +372,11 @@ def moe_lora_layer(x, base: FrozenExperts, a_g, b_g, a_u, b_u, a_d, b_d, *, k: i
         raise ValueError("x must be a bf16 CUDA tensor")
     if logits is None and base.w_r is None:
         raise ValueError("either router weights or logits are required")
+    if (a_u is None) != (b_u is None):
+        raise ValueError("a_u and b_u are both given (gate and up adapters) or both None "
+                         "(one gate|up adapter)")
+    if a_u is None and (b_g.shape[-1] != 2 * base.ffn or a_g.shape[-1] != b_g.shape[-2]):
+        raise ValueError("a gate|up adapter is a_g [E, H, r], b_g [E, r, 2F]")
     a_r = b_r = None
     scale_r = 1.0
     if router_lora is not None:
@@ -359,10 +389,21 @@ def moe_lora_layer(x, base: FrozenExperts, a_g, b_g, a_u, b_u, a_d, b_d, *, k: i
     if x.shape[0] == 0:
         # No tokens: zeros that stay in the autograd graph (every LoRA factor
         # gets a zero gradient), as the reference's empty-input paths do
-        # (runtime/bridge_runtime.py:812-823, lora.py:831-832).
+        # (runtime/bridge_runtime.py:812-823, lora.py:831-832).  With
+        # fuse_main_grad and an fp32 main_grad on every factor, the factors'
+        # (zero) gradients are already "in" main_grad: they are marked as such
+        # and stay out of the graph, so autograd hands them None as on the
+        # non-empty fused path.
+        factors = [p for p in (a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r) if p is not None]
+        fused = fuse_main_grad and all(
+            getattr(p, "main_grad", None) is not None and p.main_grad.dtype == torch.float32
+            and p.main_grad.shape == p.shape for p in factors)
         zero = x.sum() * 0.0
-        for p in (a_g, b_g, a_u, b_u, a_d, b_d, a_r, b_r):
-            if p is not None:
+        if fused:
+            for p in factors:
+                p.grad_added_to_main_grad = True
+        else:
+            for p in factors:
                 zero = zero + p.sum().to(x.dtype) * 0.0
         y = zero.expand(0, x.shape[1]).clone()
         idx = torch.zeros((0, k), dtype=torch.int32, device=x.device)

@@ -233,9 +233,15 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
     ``b_scale``; the fp8 MFMA computes s_a s_b (A_q B_q^T).
     """
     _cuda(a, b, seg, a_rows, tl, l, b_scale, a_scale)
-    _need(a.dtype == torch.bfloat16 or (a_scale is not None and a.dtype in FP8_DTYPES),
-          "A must be bf16 (or fp8 with a_scale)")
-    fmt, bsc, bs_es = _weight_format(b, b_scale, scale_per_k, a_scale)
+    f16 = a.dtype == torch.float16
+    _need(a.dtype == torch.bfloat16 or f16 or (a_scale is not None and a.dtype in FP8_DTYPES),
+          "A must be bf16, fp16 (or fp8 with a_scale)")
+    if f16:   # fp16 operands throughout (the operator drop-ins accept fp16)
+        _need(b.dtype == torch.float16 and b_scale is None and a_scale is None,
+              "fp16 A needs fp16 B and no scales")
+        fmt, bsc, bs_es = _lib.F16, None, 0
+    else:
+        fmt, bsc, bs_es = _weight_format(b, b_scale, scale_per_k, a_scale)
     _need(b.dim() == 3 and b.shape[0] == num_experts, "B must be [E, N, K]")
     n, k = b.shape[1], b.shape[2]
     _need(a.shape[-1] == k, f"A has K={a.shape[-1]}, B has K={k}")
@@ -246,10 +252,14 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
     if tl is not None:
         kt = tl.shape[1]
         _need(l is not None and l.shape == (num_experts, n, kt), "L must be [E, N, kt]")
-        _need(tl.dtype == torch.bfloat16 and l.dtype == torch.bfloat16, "LoRA operands must be bf16")
+        lt = torch.float16 if f16 else torch.bfloat16
+        _need(tl.dtype == lt and l.dtype == lt, f"LoRA operands must be {lt}")
         ldt, ldl, l_es = _rowmajor(tl, "Tl"), _rowmajor(l, "L"), l.stride(0)
     if out is None:
-        out = torch.empty((m, n), dtype=torch.float32 if out_fp32 else torch.bfloat16, device=a.device)
+        out = torch.empty((m, n), dtype=torch.float32 if out_fp32 else
+                          (torch.float16 if f16 else torch.bfloat16), device=a.device)
+    _need(out.dtype == torch.float32 or out.dtype == (torch.float16 if f16 else torch.bfloat16),
+          "C must be fp32 or the operands' 16-bit type")
     call("art_moe_grouped_gemm", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(a_scale), ptr(b),
          _rowmajor(b, "B"),
          b.stride(0), ptr(bsc), bs_es, fmt, ptr(tl), ldt, ptr(l), ldl, l_es, kt, ptr(seg),
@@ -327,13 +337,16 @@ def quantize_rows_fp8(src: torch.Tensor, *, rows: torch.Tensor | None = None,
     """(q [M, K] float8_e4m3fn, row_scale [M] fp32): per-row e4m3fn quantisation
     of bf16 rows ``src[rows[m]]`` (or ``src[m]``), optionally times the
     per-expert column scales ``col_scale`` [E, K] of row m's expert segment in
-    ``seg``.  row_scale = amax / 448 (1 for a zero row)."""
+    ``seg``.  row_scale = amax / 448 (1 for a zero row).  With ``seg``, rows
+    past the last segment are zero with scale 1 (nothing is gathered)."""
     _cuda(src, rows, seg, col_scale)
     _need(src.dtype == torch.bfloat16 and src.dim() == 2, "src must be bf16 [rows, K]")
     k = src.shape[1]
     if m is None:
         m = rows.shape[0] if rows is not None else src.shape[0]
     cs_es = 0
+    if seg is not None and not num_experts:
+        num_experts = _lib.experts_of_seg(seg)
     if col_scale is not None:
         _need(col_scale.dtype == torch.float32 and col_scale.is_contiguous() and col_scale.dim() == 2
               and col_scale.shape[1] == k and seg is not None, "col_scale must be fp32 [E, K] with seg")
@@ -365,12 +378,18 @@ def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_expe
     if out is None:
         shape = (num_experts, q, p) if transpose_out else (num_experts, p, q)
         out = torch.empty(shape, dtype=out_dtype, device=lm.device)
-    _need(out.dtype in (torch.float32, torch.bfloat16), "wgrad output must be fp32 or bf16")
+    f16 = lm.dtype == torch.float16
+    _need(lm.dtype in (torch.bfloat16, torch.float16) and r.dtype == lm.dtype,
+          "wgrad operands must both be bf16 or both fp16")
+    half = torch.float16 if f16 else torch.bfloat16
+    _need(out.dtype in (torch.float32, half), f"wgrad output must be fp32 or {half}")
     _need(not (accumulate and out.dtype != torch.float32), "wgrad accumulates into fp32 only")
     if accumulate:
         mode = _lib.WGRAD_ACCUMULATE
     else:
-        mode = _lib.WGRAD_STORE_BF16 if out.dtype == torch.bfloat16 else _lib.WGRAD_STORE
+        mode = _lib.WGRAD_STORE_BF16 if out.dtype == half else _lib.WGRAD_STORE
+    if f16:
+        mode |= _lib.WGRAD_F16
     def strides(o):
         if o is None:
             return 0, 0, 0
@@ -415,8 +434,9 @@ def transposed(src: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
 def pack(*items) -> None:
     """Batched strided copies in one launch (at most 16 per call).
 
-    Each item is ``(dst, src, scale)``: ``dst`` an [E, R, C] bf16 view with a
-    contiguous last dimension, ``src`` an [E, Rs, Cs] bf16 view with any
+    Each item is ``(dst, src, scale)``: ``dst`` an [E, R, C] bf16 (or, for
+    every item alike, fp16) view with a contiguous last dimension, ``src`` an
+    [E, Rs, Cs] view of the same type with any
     strides (a ``.transpose(1, 2)`` view reads transposed) or None.  Writes
     ``dst[e, r, c] = scale * src[e, r, c]`` where ``r < Rs`` and ``c < Cs``,
     zero elsewhere.
@@ -424,24 +444,27 @@ def pack(*items) -> None:
     _need(len(items) <= _lib.PACK_MAX, f"pack takes at most {_lib.PACK_MAX} copies")
     descs = (_lib.PackDesc * max(len(items), 1))()
     dev = None
+    dt = items[0][0].dtype if items else torch.bfloat16
+    _need(dt in (torch.bfloat16, torch.float16), "pack copies bf16 or fp16 elements")
     for i, (dst, src, scale) in enumerate(items):
         _cuda(dst, src)
-        _need(dst.dim() == 3 and dst.dtype == torch.bfloat16 and dst.stride(2) == 1,
-              "pack destination must be an [E, R, C] bf16 view with contiguous last dim")
+        _need(dst.dim() == 3 and dst.dtype == dt and dst.stride(2) == 1,
+              "pack destination must be an [E, R, C] view of one 16-bit type with contiguous last dim")
         e, rr, cc = dst.shape
         d = descs[i]
         d.dst, d.d_es, d.d_rs = dst.data_ptr(), dst.stride(0), dst.stride(1)
         d.E, d.R, d.C, d.scale = e, rr, cc, float(scale)
         if src is not None:
-            _need(src.dim() == 3 and src.dtype == torch.bfloat16 and src.shape[0] == e,
-                  "pack source must be an [E, Rs, Cs] bf16 view")
+            _need(src.dim() == 3 and src.dtype == dt and src.shape[0] == e,
+                  "pack source must be an [E, Rs, Cs] view of the destination's type")
             _need(src.shape[1] <= rr and src.shape[2] <= cc, "pack source larger than destination")
             d.src = src.data_ptr()
             d.s_es, d.s_rs, d.s_cs = src.stride(0), src.stride(1), src.stride(2)
             d.src_r, d.src_c = src.shape[1], src.shape[2]
         dev = dst.device
     if items:
-        call("art_moe_pack", ctypes.cast(descs, ctypes.c_void_p), len(items), stream_ptr(dev))
+        call("art_moe_pack_typed", ctypes.cast(descs, ctypes.c_void_p), len(items),
+             int(dt == torch.float16), stream_ptr(dev))
 
 
 # ------------------------------------------------------------- router LoRA

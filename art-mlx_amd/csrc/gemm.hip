@@ -318,15 +318,35 @@ __device__ __forceinline__ bf16x8 scale_frag(bf16x8 v, float s) {
 }
 
 // B is the MFMA's first operand: acc[i][j] accumulates the transposed block,
-// so each lane ends up with 4 consecutive output columns of one row.
-template <int TM, int TN>
+// so each lane ends up with 4 consecutive output columns of one row.  The
+// fragments are 16-bit values of either type (F16: IEEE half operands, the
+// fp16 MFMA; otherwise bfloat16).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <int TM, int TN, bool F16 = false>
 __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&af)[TM],
                                          const bf16x8 (&bfv)[TN]) {
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfv[j], af[i], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < TN; ++j) {
+      if constexpr (F16)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bfv[j]),
+                                                           __builtin_bit_cast(f16x8, af[i]),
+                                                           acc[i][j], 0, 0, 0);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfv[j], af[i], acc[i][j], 0, 0, 0);
+    }
+}
+
+// Four fp32 values rounded to IEEE half, packed into 8 bytes.
+__device__ __forceinline__ uint2 pack4h(float a, float b, float c, float d) {
+  auto h2 = [](float x, float y) {
+    const uint16_t ux = __builtin_bit_cast(uint16_t, (_Float16)x);
+    const uint16_t uy = __builtin_bit_cast(uint16_t, (_Float16)y);
+    return (uint32_t)ux | ((uint32_t)uy << 16);
+  };
+  return make_uint2(h2(a, b), h2(c, d));
 }
 
 // Row groups of the SwiGLU-backward epilogue: the fewest that divide the
@@ -338,7 +358,8 @@ constexpr int epi2_groups(int tm, int bm, int bn, int lds_bytes) {
   return 0;
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64,
+          bool F16 = false>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -371,6 +392,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int EPI2_NH = EPI == EPI_SWIGLU_BWD ? epi2_groups(TM, BM, BN, LDS_BYTES) : 1;
   static_assert(EPI2_NH >= 1, "SwiGLU backward staging (dg and du of a row group) must fit the LDS ring");
   static_assert(!W8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
+  static_assert(!F16 || (EPI == EPI_STORE && BQ8 == B_BF16), "fp16 operands: plain store products");
 
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES];
   float *sRed = (float *)(smem + LDS_BYTES);
@@ -398,7 +420,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     }
     const int e = lo;
     const int m0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
-    const int m_end = p.seg_off[e + 1];
+    // Rows of the segment, never past the M rows of A / C (a segment table
+    // whose counts sum to more than M must not send the kernel past them).
+    const int m_end = min(p.seg_off[e + 1], (int)p.M);
 
     // Source rows of this lane's DMA slots (clamped into the segment / N), as
     // 32-bit byte offsets from wave-uniform bases (the host checks that every
@@ -563,14 +587,14 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         const char *st = smem + (ks % STAGES) * STAGE_BYTES;
         load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, 1, wm, wn, lrow, lk, af1, bf1);
         __builtin_amdgcn_sched_barrier(0);
-        mma_step<TM, TN>(acc, af0, bf0);
+        mma_step<TM, TN, F16>(acc, af0, bf0);
         __builtin_amdgcn_sched_barrier(0);
         if (ks + 1 < nk) ART_STAGE_IN_STAGGERED(ks + 1);
         if (ks + 1 < nk_full)
           load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem + ((ks + 1) % STAGES) * STAGE_BYTES, 0,
                                                     wm, wn, lrow, lk, af0, bf0);
         __builtin_amdgcn_sched_barrier(0);
-        mma_step<TM, TN>(acc, af1, bf1);
+        mma_step<TM, TN, F16>(acc, af1, bf1);
         __builtin_amdgcn_sched_barrier(0);
         if (late_issue && ks + STAGES < nk) ART_ISSUE(ks + STAGES);
       }
@@ -589,11 +613,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 0, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 1, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
         ART_FENCE();
-        mma_step<TM, TN>(acc, af0, bf0);
+        mma_step<TM, TN, F16>(acc, af0, bf0);
         ART_FENCE();
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 2, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
         ART_FENCE();
-        mma_step<TM, TN>(acc, af1, bf1);
+        mma_step<TM, TN, F16>(acc, af1, bf1);
         ART_FENCE();
         if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
         ART_FENCE();
@@ -602,20 +626,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1);
         ART_FENCE();
-        mma_step<TM, TN>(acc, af0, bf0);
+        mma_step<TM, TN, F16>(acc, af0, bf0);
         ART_FENCE();
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
         ART_FENCE();
-        mma_step<TM, TN>(acc, af1, bf1);
+        mma_step<TM, TN, F16>(acc, af1, bf1);
         ART_FENCE();
         if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
         ART_FENCE();
         load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
       }
       ART_FENCE();
-      mma_step<TM, TN>(acc, af0, bf0);
+      mma_step<TM, TN, F16>(acc, af0, bf0);
       ART_FENCE();
-      mma_step<TM, TN>(acc, af1, bf1);
+      mma_step<TM, TN, F16>(acc, af1, bf1);
 #undef ART_FENCE
     }
     }
@@ -637,7 +661,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) bfv[j] = scale_frag(bfv[j], 1.0f / bsc[j]);
         }
-        mma_step<TM, TN>(acc, af, bfv);
+        mma_step<TM, TN, F16>(acc, af, bfv);
       }
     }
 #undef ART_STAGE_IN
@@ -701,9 +725,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
             for (int q = 0; q < 4; ++q) {
               const int row = wm * WTM + i * 32 + lrow;
               const int unit = (wn * WTN + j * 32) / 4 + 2 * q + lk;
-              stage_unit(row, unit,
-                         pack4(p.alpha * acc[i][j][4 * q], p.alpha * acc[i][j][4 * q + 1],
-                               p.alpha * acc[i][j][4 * q + 2], p.alpha * acc[i][j][4 * q + 3]));
+              const float v0 = p.alpha * acc[i][j][4 * q], v1 = p.alpha * acc[i][j][4 * q + 1];
+              const float v2 = p.alpha * acc[i][j][4 * q + 2], v3 = p.alpha * acc[i][j][4 * q + 3];
+              stage_unit(row, unit, F16 ? pack4h(v0, v1, v2, v3) : pack4(v0, v1, v2, v3));
             }
         barrier_nofence();
         bf16 *c = (bf16 *)p.c;
@@ -860,7 +884,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 }
 
 
-template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64>
+template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64,
+          bool F16 = false>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
                      const char *what) {
   constexpr int bmi = BM / 64 - 1;  // segment-table row of this tile height
@@ -871,7 +896,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   if (occ == 0) {
     int o = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8, BK>, NT, 0) != hipSuccess ||
+            &o, gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8, BK, F16>, NT, 0) != hipSuccess ||
         o < 1)
       o = 1;
     occ = o;
@@ -885,7 +910,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   if (grid > max_tiles) grid = max_tiles;
   if (grid >= 8) grid &= ~(int64_t)7;
   if (grid < 1) grid = 1;
-  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8, BK><<<dim3((unsigned)grid), NT, 0, s>>>(p);
+  gemm_nt_kernel<BM, BN, WM, WN, STAGES, EPI, BQ8, BK, F16><<<dim3((unsigned)grid), NT, 0, s>>>(p);
   return check_launch(what);
 }
 
@@ -999,7 +1024,7 @@ static int check_fp8(int32_t fmt, const void *b, int64_t ldb, const float *b_sca
                      const char *who) {
   ART_REQUIRE(fmt == ART_MOE_B_BF16 || fmt == ART_MOE_B_FP8_ROWSCALE ||
                   fmt == ART_MOE_B_FP8_KSCALE || fmt == ART_MOE_AB_FP8,
-              "%s: unknown weight format %d", who, fmt);
+              "%s: unknown weight format %d", who, fmt);  // (ART_MOE_F16: grouped_gemm only)
   if (fmt == ART_MOE_AB_FP8) {
     ART_REQUIRE(K % 64 == 0, "%s: fp8 operands need K a multiple of 64 (K=%d)", who, K);
     ART_REQUIRE(ldb % 16 == 0 && lda % 16 == 0,
@@ -1030,8 +1055,13 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   clear_error();
   int rc = check_common(a, lda, b, ldb, seg, E, M, K, kt, tl, ldt, l, ldl, "grouped_gemm");
   if (rc) return rc;
-  rc = check_fp8(b_format, b, ldb, b_scale, bs_estride, K, N, lda, a_scale, "grouped_gemm");
-  if (rc) return rc;
+  const bool f16 = b_format == ART_MOE_F16;
+  if (f16) {
+    ART_REQUIRE(!a_scale && !b_scale, "grouped_gemm: fp16 operands take no scales");
+  } else {
+    rc = check_fp8(b_format, b, ldb, b_scale, bs_estride, K, N, lda, a_scale, "grouped_gemm");
+    if (rc) return rc;
+  }
   ART_REQUIRE(N > 0 && N % 8 == 0 && (c || M == 0),
               "grouped_gemm: need N a positive multiple of 8 and an output");
   ART_REQUIRE(ldc >= N && ldc % 8 == 0 && aligned16(c),
@@ -1047,6 +1077,12 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   p.l = kt ? (const bf16 *)l : nullptr; p.ldl = ldl; p.l_es = l_estride; p.kt = kt;
   p.E = E; p.N = N; p.K = K; p.alpha = alpha; p.c = c; p.ldc = ldc; p.c_fp32 = c_fp32; p.M = M;
   hipStream_t s = as_stream(stream);
+  if (f16) {  // fp16 operands (the reference operators accept fp16 or bf16)
+    if (N <= 32) return launch_nt<128, 32, 4, 1, 4, EPI_STORE, B_BF16, 64, true>(p, seg, M, s, "grouped_gemm/f16/n32");
+    if (N <= 64) return launch_nt<128, 64, 4, 1, 4, EPI_STORE, B_BF16, 64, true>(p, seg, M, s, "grouped_gemm/f16/n64");
+    if (N <= 128) return launch_nt<128, 128, 2, 2, 4, EPI_STORE, B_BF16, 64, true>(p, seg, M, s, "grouped_gemm/f16/n128");
+    return launch_nt<256, 256, 2, 4, 2, EPI_STORE, B_BF16, 64, true>(p, seg, M, s, "grouped_gemm/f16");
+  }
   if (b_format != ART_MOE_B_BF16) return launch_fp8<EPI_STORE>(b_format, p, seg, M, s, "grouped_gemm/fp8");
   if (N <= 32) return launch_nt<128, 32, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n32");
   if (N <= 64) return launch_nt<128, 64, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n64");

@@ -42,6 +42,11 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(
   const int lane = lane_id();
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;
+  if (seg && m >= seg[E]) {  // past every segment: no source row
+    for (int k = lane * 8; k < K; k += kWave * 8) *(uint2 *)(q + m * ldq + k) = make_uint2(0u, 0u);
+    if (lane == 0) row_scale[m] = 1.0f;
+    return;
+  }
   const bf16 *x = src + (int64_t)(rows ? rows[m] : m) * lds;
   const float *c = nullptr;
   if (cs) {  // expert of row m: the last e with seg[e] <= m
@@ -91,6 +96,11 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
   const int lane = lane_id();
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;
+  if (seg && m >= seg[E]) {  // past every segment: no source row
+    for (int k = lane * 8; k < K; k += kWave * 8) *(uint2 *)(q + m * ldq + k) = make_uint2(0u, 0u);
+    if (lane == 0) row_scale[m] = 1.0f;
+    return;
+  }
   const bf16 *x = src + (int64_t)(rows ? rows[m] : m) * lds;
   const float *c = nullptr;
   if (cs) {  // expert of row m: the last e with seg[e] <= m
@@ -157,8 +167,9 @@ extern "C" int art_moe_quantize_rows_fp8(const void *src, int64_t ld_src, const 
               "quantize_rows_fp8: src rows must be 16-byte aligned with ld_src >= K");
   ART_REQUIRE(ldq >= K && ldq % 8 == 0 && ((uintptr_t)q & 7) == 0,
               "quantize_rows_fp8: q rows must be 8-byte aligned with ldq >= K");
+  ART_REQUIRE(!seg || E >= 1, "quantize_rows_fp8: segment offsets need E >= 1");
   if (col_scale) {
-    ART_REQUIRE(seg && E >= 1, "quantize_rows_fp8: column scales need the segment offsets");
+    ART_REQUIRE(seg, "quantize_rows_fp8: column scales need the segment offsets");
     ART_REQUIRE(cs_estride >= K && cs_estride % 4 == 0 && ((uintptr_t)col_scale & 15) == 0,
                 "quantize_rows_fp8: column scales must be 16-byte aligned rows of >= K");
   }

@@ -248,6 +248,14 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
     int32_t *__restrict__ row_token, float *__restrict__ row_prob) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= T * k) return;
+  // Rows past the last segment (one per rejected or repeated id) belong to no
+  // expert; they map to token 0 with probability 0, so a consumer that walks
+  // all T*k rows (the fp8 row quantiser) gathers in-bounds rows.  No (t, e)
+  // pair scatters there: every pos below is < seg[E].
+  if (i >= seg[E]) {
+    row_token[i] = 0;
+    if (row_prob) row_prob[i] = 0.0f;
+  }
   const int64_t t = i / k;
   const int j = (int)(i - t * k);
   const int e = idx[i];
@@ -615,6 +623,45 @@ static int pack_tc_log2(int R, int C) {
 // parked in LDS as fp32 (row pitch TC+1), and leave as 8-element runs along
 // destination rows.  Runs are 16-byte accesses where the host found strides
 // and alignment to allow it and the run is whole; element accesses otherwise.
+// 16-bit element access of pack_kernel: bfloat16, or IEEE half with F16.
+template <bool F16>
+__device__ __forceinline__ float ld16(const bf16 *p) {
+  if constexpr (F16) return (float)*(const _Float16 *)p;
+  else return (float)*p;
+}
+template <bool F16>
+__device__ __forceinline__ void st16(bf16 *p, float v) {
+  if constexpr (F16) *(_Float16 *)p = (_Float16)v;
+  else *p = (bf16)v;
+}
+template <bool F16>
+__device__ __forceinline__ void unpack8t(const U4 &u, float *f) {
+  if constexpr (F16) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
+      f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+    }
+  } else {
+    unpack8(u, f);
+  }
+}
+template <bool F16>
+__device__ __forceinline__ U4 pack8t(const float *f) {
+  if constexpr (F16) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[2 * i]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[2 * i + 1]) << 16);
+    return U4{w[0], w[1], w[2], w[3]};
+  } else {
+    return pack8(f);
+  }
+}
+
+template <bool F16>
 __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
   __shared__ float tile[kPackTile + 256];
   const int b = blockIdx.x;
@@ -643,13 +690,13 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
     const int fa = cfast ? cb : rb, sa = cfast ? rb : cb;
     const bf16 *p = src + (int64_t)rb * d.s_rs + (int64_t)cb * d.s_cs;
     if (sa < slow_lim && vr && fa + 8 <= fast_lim) {
-      unpack8(*(const U4 *)p, v[j]);
+      unpack8t<F16>(*(const U4 *)p, v[j]);
 #pragma unroll
       for (int t = 0; t < 8; ++t) v[j][t] *= d.scale;
     } else {
 #pragma unroll
       for (int t = 0; t < 8; ++t)
-        v[j][t] = (sa < slow_lim && fa + t < fast_lim) ? d.scale * (float)p[t * fstride] : 0.0f;
+        v[j][t] = (sa < slow_lim && fa + t < fast_lim) ? d.scale * ld16<F16>(p + t * fstride) : 0.0f;
     }
   }
 #pragma unroll
@@ -676,11 +723,11 @@ __global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
     for (int t = 0; t < 8; ++t) w[t] = tile[rr * pitch + cc0 + t];
     bf16 *q = dst + (int64_t)r * d.d_rs + c;
     if (vw && c + 8 <= d.C) {
-      *(U4 *)q = pack8(w);
+      *(U4 *)q = pack8t<F16>(w);
     } else {
 #pragma unroll
       for (int t = 0; t < 8; ++t)
-        if (c + t < d.C) q[t] = (bf16)w[t];
+        if (c + t < d.C) st16<F16>(q + t, w[t]);
     }
   }
 }
@@ -888,6 +935,11 @@ extern "C" int art_moe_transpose(const void *src, int32_t E, int32_t R, int32_t 
 }
 
 extern "C" int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *stream) {
+  return art_moe_pack_typed(descs, n, 0, stream);
+}
+
+extern "C" int art_moe_pack_typed(const art_moe_pack_desc *descs, int32_t n, int32_t f16,
+                                  void *stream) {
   clear_error();
   ART_REQUIRE(n >= 0 && n <= ART_MOE_PACK_MAX, "pack: need 0 <= n <= %d (n=%d)", ART_MOE_PACK_MAX, n);
   if (n == 0) return ART_MOE_OK;
@@ -917,6 +969,7 @@ extern "C" int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *str
     a.tile_start[k + 1] = (int32_t)tiles;
   }
   if (tiles == 0) return ART_MOE_OK;
-  pack_kernel<<<dim3((unsigned)tiles), 256, 0, as_stream(stream)>>>(a);
+  if (f16) pack_kernel<true><<<dim3((unsigned)tiles), 256, 0, as_stream(stream)>>>(a);
+  else pack_kernel<false><<<dim3((unsigned)tiles), 256, 0, as_stream(stream)>>>(a);
   return check_launch("pack");
 }

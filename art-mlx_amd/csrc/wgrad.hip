@@ -64,6 +64,8 @@ struct WArgs {
   int mode;    // ART_MOE_WGRAD_STORE / _ACCUMULATE / _STORE_BF16
   float *ws;   // partial tiles of multi-chunk experts
   int n_pt, n_qt;
+  int M;       // rows of the operands (row maps)
+  int f16;     // operands (and a 16-bit output) are IEEE fp16
 };
 
 __device__ __forceinline__ void wg_store(const WArgs &a, int e, int p, int q, float acc) {
@@ -74,7 +76,8 @@ __device__ __forceinline__ void wg_store(const WArgs &a, int e, int p, int q, fl
       : (int64_t)e * a.o_es + (int64_t)p * a.o_sp + (int64_t)q * a.o_sq;
   const float val = a.alpha * acc;
   if (a.mode == ART_MOE_WGRAD_STORE_BF16) {
-    ((bf16 *)base)[off] = (bf16)val;
+    if (a.f16) ((_Float16 *)base)[off] = (_Float16)val;
+    else ((bf16 *)base)[off] = (bf16)val;
   } else {
     float *o = (float *)base + off;
     *o = a.mode == ART_MOE_WGRAD_ACCUMULATE ? *o + val : val;
@@ -139,7 +142,9 @@ __device__ __forceinline__ bf16x8 wg_frag(const char *lo_p, const char *hi_p, in
 
 // WP x WQ compute waves, each owning TP x TQ blocks of 16x16 outputs, and NP
 // DMA waves that issue every global->LDS copy of the ring.
-template <int BQ, int WP, int WQ, int TP, int TQ, int NP>
+typedef _Float16 wg_f16x8 __attribute__((ext_vector_type(8)));
+
+template <int BQ, int WP, int WQ, int TP, int TQ, int NP, bool F16>
 __global__ __launch_bounds__((WP * WQ + NP) * 64) void wgrad_kernel(const WArgs a) {
   constexpr int kWgBP = wg_bp(BQ), NW = WP * WQ, kWgThreads = (NW + NP) * 64;
   static_assert(WP * TP * 16 == kWgBP && WQ * TQ * 16 == BQ, "tile");
@@ -173,8 +178,9 @@ __global__ __launch_bounds__((WP * WQ + NP) * 64) void wgrad_kernel(const WArgs 
   const int e = lo;
   const int nce = cpre[e + 1] - cpre[e];
   const int m0 = a.seg[e] + (c - cpre[e]) * kWgChunkRows;
-  const int m1 = min(a.seg[e + 1], m0 + kWgChunkRows);
-  const int nrows = m1 - m0;  // >= 1
+  // never past the M rows of the operands (counts summing to more than M)
+  const int m1 = min(min(a.seg[e + 1], m0 + kWgChunkRows), a.M);
+  const int nrows = max(m1 - m0, 0);  // 0 only when the chunk lies past M
   const int p0 = ty * kWgBP, q0 = tz * BQ;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool dma_wave = wave >= NW;   // wave-uniform role
@@ -188,6 +194,9 @@ __global__ __launch_bounds__((WP * WQ + NP) * 64) void wgrad_kernel(const WArgs 
     rrow_s[i] = a.r_rows ? a.r_rows[m0 + i] : m0 + i;
   }
   __syncthreads();
+  // A chunk past M of a multi-chunk expert has no partial slot to fill (the
+  // reduce kernel sums only the chunks that start below M).
+  if (nrows == 0 && nce != 1) return;
 
   auto next_stage = [](int sb) { return sb + STAGE == kWgStages * STAGE ? 0 : sb + STAGE; };
   const int nk = (nrows + kWgBK - 1) / kWgBK;
@@ -246,6 +255,7 @@ __global__ __launch_bounds__((WP * WQ + NP) * 64) void wgrad_kernel(const WArgs 
       }
     };
     int s_iss = 0;
+    if (nk == 0) return;  // no rows: the compute waves take no barrier either
 #pragma unroll
     for (int s = 0; s < kWgStages - 1; ++s)
       if (s < nk) {
@@ -303,19 +313,26 @@ __global__ __launch_bounds__((WP * WQ + NP) * 64) void wgrad_kernel(const WArgs 
       for (int i = 0; i < TP; ++i)
 #pragma unroll
         for (int jj = 0; jj < TQ; ++jj)
-          acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bq[jj], acc[i][jj], 0, 0, 0);
+          if constexpr (F16)
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(wg_f16x8, af[i]),
+                                                                __builtin_bit_cast(wg_f16x8, bq[jj]),
+                                                                acc[i][jj], 0, 0, 0);
+          else
+            acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bq[jj], acc[i][jj], 0, 0, 0);
     }
   };
 
-  int s_comp = 0;
-  for (int ks = 0; ks < nk - 1; ++ks) {
+  if (nk > 0) {  // workgroup-uniform; with no rows the tile is zero
+    int s_comp = 0;
+    for (int ks = 0; ks < nk - 1; ++ks) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      compute(__builtin_amdgcn_readfirstlane(s_comp), kWgBK, std::false_type{});
+      s_comp = next_stage(s_comp);
+    }
+    // last step: rows past the chunk masked
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    compute(__builtin_amdgcn_readfirstlane(s_comp), kWgBK, std::false_type{});
-    s_comp = next_stage(s_comp);
+    compute(__builtin_amdgcn_readfirstlane(s_comp), nrows - (nk - 1) * kWgBK, std::true_type{});
   }
-  // last step: rows past the chunk masked
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  compute(__builtin_amdgcn_readfirstlane(s_comp), nrows - (nk - 1) * kWgBK, std::true_type{});
 
   // Accumulator element v of a 16x16 block: row 4*(lane/16) + v, column lane%16.
   // (a multi-chunk expert without workspace means M understated the rows:
@@ -353,6 +370,9 @@ __global__ __launch_bounds__(kWgRedThreads) void wgrad_reduce_kernel(const WArgs
   const int c0 = cpre[e], nce = cpre[e + 1] - c0;
   if (nce == 1 || (nce == 0 && a.mode == ART_MOE_WGRAD_ACCUMULATE)) return;
   if (nce > 1 && a.ws == nullptr) return;
+  // chunks that start below M (the others hold no partial)
+  const int below = a.M > a.seg[e] ? (a.M - a.seg[e] + kWgChunkRows - 1) / kWgChunkRows : 0;
+  const int nsum = min(nce, below);
   const int tile = blockIdx.x / PIECES, piece = blockIdx.x - tile * PIECES;
   const int ty = tile % a.n_pt, tz = tile / a.n_pt;
   const int t = (piece * kWgRedThreads + threadIdx.x) * 4;  // element in the tile
@@ -365,15 +385,15 @@ __global__ __launch_bounds__(kWgRedThreads) void wgrad_reduce_kernel(const WArgs
     // order as a plain loop: the sum is identical, the loads overlap)
     const size_t cstride = (size_t)a.n_pt * a.n_qt * (kWgBP * BQ);
     const float *src = a.ws + (((size_t)c0 * a.n_pt + ty) * a.n_qt + tz) * (size_t)(kWgBP * BQ) + t;
-    for (int cb = 0; cb < nce; cb += 8) {
+    for (int cb = 0; cb < nsum; cb += 8) {
       f32x4 v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        v[u] = cb + u < nce ? *(const f32x4 *)(src + (size_t)(cb + u) * cstride)
-                            : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[u] = cb + u < nsum ? *(const f32x4 *)(src + (size_t)(cb + u) * cstride)
+                             : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (cb + u < nce) s += v[u];
+        if (cb + u < nsum) s += v[u];
     }
   }
 #pragma unroll
@@ -389,13 +409,15 @@ static int64_t wgrad_max_chunks(int64_t M, int E) {
 
 template <int BQ, int WP, int WQ, int TP, int TQ, int NP>
 static int launch_wgrad(WArgs a, int64_t M, hipStream_t s) {
+  auto kern = a.f16 ? wgrad_kernel<BQ, WP, WQ, TP, TQ, NP, true>
+                    : wgrad_kernel<BQ, WP, WQ, TP, TQ, NP, false>;
   a.n_pt = (a.P + wg_bp(BQ) - 1) / wg_bp(BQ);
   a.n_qt = (a.Q + BQ - 1) / BQ;
   if (M > 0) {
     const int64_t groups = (wgrad_max_chunks(M, a.E) + 7) / 8;  // chunk groups of 8 (one per XCD)
     const int64_t blocks = groups * 8 * a.n_pt * a.n_qt;
     ART_REQUIRE(blocks < (int64_t)1 << 31, "grouped_wgrad: too many tiles");
-    wgrad_kernel<BQ, WP, WQ, TP, TQ, NP><<<dim3((unsigned)blocks), (WP * WQ + NP) * 64, 0, s>>>(a);
+    kern<<<dim3((unsigned)blocks), (WP * WQ + NP) * 64, 0, s>>>(a);
     if (int rc = check_launch("grouped_wgrad")) return rc;
   }
   constexpr int pieces = wg_bp(BQ) * BQ / (4 * kWgRedThreads);
@@ -433,6 +455,8 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   ART_REQUIRE(((lm && r) || M == 0) && seg && out, "grouped_wgrad: null pointer");
   ART_REQUIRE(((uintptr_t)lm & 15) == 0 && ((uintptr_t)r & 15) == 0,
               "grouped_wgrad: operands must be 16-byte aligned");
+  const int f16 = (mode & ART_MOE_WGRAD_F16) != 0;
+  mode &= ~ART_MOE_WGRAD_F16;
   ART_REQUIRE(mode == ART_MOE_WGRAD_STORE || mode == ART_MOE_WGRAD_ACCUMULATE ||
                   mode == ART_MOE_WGRAD_STORE_BF16,
               "grouped_wgrad: unknown mode %d", mode);
@@ -451,6 +475,8 @@ extern "C" int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t 
   a.out2 = out2; a.q_split = out2 ? q_split : Q;
   a.o2_es = o2_es; a.o2_sp = o2_ps; a.o2_sq = o2_qs;
   a.ws = (float *)workspace;
+  a.M = (int)M;
+  a.f16 = f16;
   hipStream_t s = as_stream(stream);
   switch (wgrad_bq(Q)) {
     case 16: return launch_wgrad<16, 4, 1, 2, 1, 2>(a, M, s);

@@ -72,6 +72,10 @@ extern "C" {
 #define ART_MOE_B_FP8_ROWSCALE 1
 #define ART_MOE_B_FP8_KSCALE 2
 #define ART_MOE_AB_FP8 3
+/* art_moe_grouped_gemm only: A, B, Tl, L and a 16-bit C are IEEE fp16 (the
+ * fp16 MFMA, fp32 accumulation); the reference's grouped LoRA operators accept
+ * fp16 as well as bf16 (cute_grouped_lora_quack.py:155-158). */
+#define ART_MOE_F16 4
 #define ART_MOE_SEG_LEN(E) ((1 + ART_MOE_SEG_NBM) * ((E) + 1))
 
 /* Library version, e.g. 100 for 0.1.0. */
@@ -137,7 +141,11 @@ size_t art_moe_plan_workspace_bytes(int64_t T, int32_t E);
  * row_token[M] (token of each permuted row, M = T*k), and, if w != NULL,
  * row_prob[M] = w[t,j] of the row.  Out-of-range or repeated ids add to
  * *status (caller-zeroed) and are dropped (rows of the segment table then
- * sum to less than M).
+ * sum to less than M); the rows m >= seg[E] left over at the end get
+ * row_token[m] = 0 and row_prob[m] = 0, so every entry of both maps is
+ * defined.  An id of -1 counts like any other rejected id: a caller that
+ * feeds the output of art_moe_router_replay (which already counted it) passes
+ * a separate status here.
  * Replaces: moe_utils.permute's sorted_indices / tokens_per_expert
  * (routing_map.sum(0)) with moe_permute_fusion=True (provider.py:604). */
 int art_moe_dispatch_plan(const int32_t *idx, const float *w, int64_t T,
@@ -254,6 +262,9 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
 #define ART_MOE_WGRAD_STORE 0
 #define ART_MOE_WGRAD_ACCUMULATE 1
 #define ART_MOE_WGRAD_STORE_BF16 2
+/* Flag OR-ed into the mode: Lm and R are fp16 (fp16 MFMA); _STORE_BF16 then
+ * writes fp16. */
+#define ART_MOE_WGRAD_F16 16
 
 /* Segmented "TN" product (LoRA weight gradients, fp32 accumulation):
  *   out[e*o_es + p*o_ps + q*o_qs] (+)=
@@ -265,7 +276,10 @@ int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
  * [E][Q][P].  mode: ART_MOE_WGRAD_STORE writes fp32 out, _ACCUMULATE adds to
  * fp32 out, _STORE_BF16 writes bf16 out (one rounding of the fp32 sum: the
  * parameter-dtype gradient the reference returns).
- * M is the number of segment rows (>= seg[E]).  Segments are processed in
+ * M is the number of rows of the operands' row maps (normally seg[E]); rows
+ * at or past M are never read (a table summing to more is cut at M; chunks
+ * wholly past M of an expert with a single chunk are not written).
+ * Segments are processed in
  * chunks of 2048 rows; chunks of segments longer than that leave fp32
  * partials in `workspace` (art_moe_wgrad_workspace_bytes), summed in chunk
  * order afterwards: results do not depend on the schedule.
@@ -364,6 +378,12 @@ typedef struct {
  * cute_grouped_lora_quack.py:205-224, 350-353, 465-468. */
 int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *stream);
 
+/* art_moe_pack for either 16-bit element type: f16 != 0 reads and writes IEEE
+ * fp16 (scale applied in fp32, one rounding), f16 == 0 is art_moe_pack.
+ * Replaces the same copies for the reference's fp16 operator inputs
+ * (cute_grouped_lora_quack.py:155-158). */
+int art_moe_pack_typed(const art_moe_pack_desc *descs, int32_t n, int32_t f16, void *stream);
+
 /* Per-row OCP e4m3fn quantisation of bf16 rows, the A operand of the
  * ART_MOE_AB_FP8 products: for m < M with v[k] = src[r][k] * cs[k],
  * r = rows ? rows[m] : m and cs = col_scale ? col_scale + e(m)*cs_estride
@@ -371,7 +391,9 @@ int art_moe_pack(const art_moe_pack_desc *descs, int32_t n, void *stream);
  *   row_scale[m] = max_k |v[k]| / 448 (1 for an all-zero row),
  *   q[m][k] = e4m3fn(v[k] / row_scale[m]) (round to nearest even).
  * col_scale folds a weight's per-k scales into the activation (data-gradient
- * products).  K % 8 == 0; src 16-byte aligned rows; q 8-byte aligned.
+ * products).  With seg, rows m >= seg[E] (past every segment) read nothing:
+ * q[m] is zero and row_scale[m] = 1.  K % 8 == 0; src 16-byte aligned rows;
+ * q 8-byte aligned.
  * No reference counterpart: the reference keeps activations in bf16. */
 int art_moe_quantize_rows_fp8(const void *src, int64_t ld_src, const int32_t *rows,
                               const int32_t *seg, int32_t E, const float *col_scale,

@@ -40,6 +40,9 @@ Pinning (tests/test_oracle_layer.py):
 * weighted_swiglu: finite differences and the closed form at g = 0.
 * router LoRA: equals the plain router with the merged weight
   W_r + s (A_r B_r)^T, and finite differences through the layer.
+* fused gate|up adapter (``a_u = b_u = None``, lora.py:1472-1497,
+  1521-1527): equals the dual form with A_g = A_u = A, B_g = B[..., :F],
+  B_u = B[..., F:] at one scale (catches a swapped or transposed half).
 """
 from __future__ import annotations
 
@@ -149,7 +152,9 @@ class LayerParams:
     w_r [E,H] router weight (frozen; None when logits are given)
     w1  [E,2F,H] FC1 base weight, gate rows first (frozen)
     w2  [E,H,F]  FC2 base weight (frozen)
-    a_g, a_u [E,H,r]; b_g, b_u [E,r,F]   gate/up LoRA (A_T, B_T layout)
+    a_g, a_u [E,H,r]; b_g, b_u [E,r,F]   gate/up LoRA (A_T, B_T layout); with
+                                        a_u = b_u = None, a_g [E,H,r], b_g [E,r,2F]
+                                        is one gate|up adapter (scale_g)
     a_d [E,F,r]; b_d [E,r,H]             down LoRA
     scale_g, scale_u, scale_d           alpha / rank
     """
@@ -158,8 +163,8 @@ class LayerParams:
     w2: torch.Tensor
     a_g: torch.Tensor
     b_g: torch.Tensor
-    a_u: torch.Tensor
-    b_u: torch.Tensor
+    a_u: torch.Tensor | None
+    b_u: torch.Tensor | None
     a_d: torch.Tensor
     b_d: torch.Tensor
     scale_g: float
@@ -191,9 +196,12 @@ def moe_lora_layer(x: torch.Tensor, p: LayerParams, k: int, *,
     # permuted probs, expert-major (megatron: probs.T.masked_select(routing_map.T))
     perm_probs = probs.t().masked_select(rmap.t())
     x_perm = permute(xw, row_token)
-    y1 = grouped_linear(x_perm, p.w1.to(dtype), counts) + grouped_lora_dual(
-        x_perm, p.a_g.to(dtype), p.b_g.to(dtype), p.a_u.to(dtype), p.b_u.to(dtype),
-        counts, p.scale_g, p.scale_u)
+    if p.a_u is None:   # one gate|up adapter: A shared, B over both halves
+        adapter = grouped_lora(x_perm, p.a_g.to(dtype), p.b_g.to(dtype), counts, p.scale_g)
+    else:
+        adapter = grouped_lora_dual(x_perm, p.a_g.to(dtype), p.b_g.to(dtype), p.a_u.to(dtype),
+                                    p.b_u.to(dtype), counts, p.scale_g, p.scale_u)
+    y1 = grouped_linear(x_perm, p.w1.to(dtype), counts) + adapter
     h = weighted_swiglu(y1, perm_probs)
     y2 = grouped_linear(h, p.w2.to(dtype), counts) + grouped_lora(
         h, p.a_d.to(dtype), p.b_d.to(dtype), counts, p.scale_d)

@@ -171,3 +171,35 @@ def test_layer_gradcheck_router_lora():
         return y
 
     assert torch.autograd.gradcheck(fn, (x, p.a_r, p.b_r), eps=1e-6, atol=1e-6)
+
+
+def test_layer_fused_gate_up_equals_dual_with_shared_a():
+    """One gate|up adapter (A shared, B over 2F columns) is the dual form with
+    A_g = A_u = A, B_g = B[:, :, :F], B_u = B[:, :, F:] at one scale; a swapped
+    or transposed half breaks the identity.  Gradients by finite differences."""
+    e, h, f, r, t, k = 4, 6, 3, 2, 6, 2
+    p = _params(e, h, f, r, seed=40)
+    x = _rand(t, h, seed=41)
+    a = _rand(e, h, r, seed=42)
+    b = _rand(e, r, 2 * f, seed=43)
+    p.a_g, p.a_u, p.b_g, p.b_u = a, a, b[:, :, :f], b[:, :, f:]
+    p.scale_u = p.scale_g
+    y_dual, _ = L.moe_lora_layer(x, p, k, dtype=D)
+    p.a_u = p.b_u = None
+    p.b_g = b
+    y_fused, _ = L.moe_lora_layer(x, p, k, dtype=D)
+    assert torch.allclose(y_fused, y_dual, atol=1e-12)
+    p.b_g = torch.cat((b[:, :, f:], b[:, :, :f]), dim=2)   # halves swapped
+    y_swapped, _ = L.moe_lora_layer(x, p, k, dtype=D)
+    assert not torch.allclose(y_swapped, y_dual, atol=1e-6)
+
+    xl = x.clone().requires_grad_()
+    al = a.clone().requires_grad_()
+    bl = b.clone().requires_grad_()
+
+    def fn(x, a, b):
+        p.a_g, p.b_g = a, b
+        y, _ = L.moe_lora_layer(x, p, k, dtype=D)
+        return y
+
+    assert torch.autograd.gradcheck(fn, (xl, al, bl), eps=1e-6, atol=1e-6)
