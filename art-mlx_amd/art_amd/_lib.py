@@ -77,6 +77,10 @@ SIGNATURES = {
                                      _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P,
                                      _SZ, _P]),
     "art_moe_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
+    "art_moe_wgrad_noalloc_scratch_bytes": (_SZ, []),
+    "art_moe_grouped_wgrad_noalloc": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32,
+                                             _F, _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64,
+                                             _I32, _P]),
     "art_moe_transpose": (_I32, [_P, _I32, _I32, _I32, _I64, _I64, _P, _I64, _I64, _F, _P]),
     "art_moe_pack": (_I32, [_P, _I32, _P]),
     "art_moe_pack_typed": (_I32, [_P, _I32, _I32, _P]),

@@ -302,6 +302,26 @@ int art_moe_grouped_wgrad(const void *lm, int64_t ldl, const int32_t *l_rows,
  * M <= 2048: no segment can span two 2048-row chunks). */
 size_t art_moe_wgrad_workspace_bytes(int64_t M, int32_t E, int32_t P, int32_t Q);
 
+/* art_moe_grouped_wgrad without a workspace argument: the partial tiles go
+ * to a static device array of art_moe_wgrad_noalloc_scratch_bytes() bytes
+ * (64 MiB) that the library holds on each GPU it runs on until the process
+ * ends.  Allocates nothing (no hipMalloc / hipFree, no allocating library
+ * call).  Sizes whose art_moe_wgrad_workspace_bytes exceed the scratch are
+ * rejected with ART_MOE_ERR_INVALID_ARG.  Every call on a GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (different streams,
+ * different threads) race and must be ordered by the caller.
+ * No counterpart in the reference: it exists for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation). */
+size_t art_moe_wgrad_noalloc_scratch_bytes(void);
+int art_moe_grouped_wgrad_noalloc(const void *lm, int64_t ldl, const int32_t *l_rows,
+                                  const void *r, int64_t ldr, const int32_t *r_rows,
+                                  const int32_t *seg, int32_t E, int64_t M, int32_t P,
+                                  int32_t Q, float alpha, void *out, int64_t o_es,
+                                  int64_t o_ps, int64_t o_qs, void *out2,
+                                  int32_t q_split, int64_t o2_es, int64_t o2_ps,
+                                  int64_t o2_qs, int32_t mode, void *stream);
+
 /* --------------------------------------------------------- weighted SwiGLU
  * Standalone forms of the SwiGLU the fused products run in their epilogues,
  * for the module-level path.  y1 bf16 [M][2F] (gate columns first), prob fp32

@@ -1,0 +1,82 @@
+"""The allocation-free weight-gradient entry point (art_moe_grouped_wgrad_noalloc)
+against art_moe_grouped_wgrad with a caller workspace, through the C ABI.
+
+Both run the same kernels in the same order, so results must be bit-identical.
+Two calls in a row share the library's static scratch: the second, smaller one
+must not see the first one's partial tiles.  Sizes beyond the scratch are
+rejected before anything is launched.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _args(lm, r, seg, e, out, l_rows=None, mode=0):
+    from art_amd._lib import ptr
+    p, q = lm.shape[1], r.shape[1]
+    m = l_rows.numel() if l_rows is not None else lm.shape[0]
+    return [ptr(lm), lm.stride(0), ptr(l_rows), ptr(r), r.stride(0), None, ptr(seg), e, m, p, q,
+            1.0, ptr(out), out.stride(0), out.stride(1), out.stride(2), None, 0, 0, 0, 0, mode]
+
+
+def _noalloc(lm, r, seg, e, out, l_rows=None, mode=0):
+    from art_amd._lib import call, stream_ptr
+    call("art_moe_grouped_wgrad_noalloc", *_args(lm, r, seg, e, out, l_rows, mode),
+         stream_ptr(lm.device))
+    return out
+
+
+def _case(device, counts, p, q, seed, gather):
+    from art_amd import ops
+    g = torch.Generator().manual_seed(seed)
+    m = sum(counts)
+    e = len(counts)
+    t = m // 2 if gather else m
+    lm = torch.randn(t, p, generator=g).to(torch.bfloat16).to(device)
+    r = torch.randn(m, q, generator=g).to(torch.bfloat16).to(device)
+    rows = torch.randint(0, t, (m,), generator=g, dtype=torch.int32).to(device) if gather else None
+    seg = ops.segments_from_counts(counts, e, device)
+    return lm, r, rows, seg, e
+
+
+def test_noalloc_wgrad_matches_workspace_entry_point(device):
+    from art_amd import _lib, ops
+    assert int(_lib.load().art_moe_wgrad_noalloc_scratch_bytes()) == 64 << 20
+    # first call: experts over several 2048-row chunks (the scratch holds partials)
+    counts = [5000, 0, 7000, 1200, 9000]
+    lm, r, rows, seg, e = _case(device, counts, 512, 32, seed=1, gather=False)
+    print(f"noalloc call 1: M={sum(counts)} E={e} P=512 Q=32", flush=True)
+    ref = ops.grouped_wgrad(lm, r, seg, e)
+    out = torch.full((e, 512, 32), float("nan"), device=device)
+    _noalloc(lm, r, seg, e, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    # second call, smaller, with gathered rows and a bf16 result
+    counts2 = [2100, 3000, 0, 4500]
+    lm2, r2, rows2, seg2, e2 = _case(device, counts2, 256, 16, seed=2, gather=True)
+    print(f"noalloc call 2: M={sum(counts2)} E={e2} P=256 Q=16 gathered, bf16 out", flush=True)
+    ref2 = ops.grouped_wgrad(lm2, r2, seg2, e2, l_rows=rows2, out_dtype=torch.bfloat16)
+    out2 = torch.empty((e2, 256, 16), dtype=torch.bfloat16, device=device)
+    _noalloc(lm2, r2, seg2, e2, out2, l_rows=rows2, mode=_lib.WGRAD_STORE_BF16)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref2)
+    # and the first case again after the second: same bits
+    _noalloc(lm, r, seg, e, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def test_noalloc_wgrad_rejects_sizes_beyond_the_scratch(device):
+    from art_amd import _lib
+    m, e, p, q = 1 << 22, 128, 4096, 128
+    need = int(_lib.load().art_moe_wgrad_workspace_bytes(m, e, p, q))
+    assert need > (64 << 20)
+    seg = torch.zeros(_lib.seg_len(e), dtype=torch.int32, device=device)
+    lm = torch.zeros(16, p, dtype=torch.bfloat16, device=device)
+    r = torch.zeros(16, q, dtype=torch.bfloat16, device=device)
+    out = torch.zeros(e, p, q, device=device)
+    args = _args(lm, r, seg, e, out)
+    args[8] = m   # claim M rows: rejected on the host before any launch
+    with pytest.raises(ValueError, match="static scratch"):
+        _lib.call("art_moe_grouped_wgrad_noalloc", *args, _lib.stream_ptr(device))
