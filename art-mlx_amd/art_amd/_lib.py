@@ -58,7 +58,8 @@ SIGNATURES = {
     "art_moe_last_error": (ctypes.c_char_p, []),
     "art_moe_router_topk": (_I32, [_P, _I64, _I32, _I32, _P, _P, _P]),
     "art_moe_router_replay": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
-    "art_moe_router_replay_rows": (_I32, [_P, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "art_moe_router_replay_rows": (_I32, [_P, _P, _I64, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _P,
+                                          _P]),
     "art_moe_router_backward": (_I32, [_P, _I32, _I64, _P, _P, _P, _I64, _I32, _I32, _P, _P, _P]),
     "art_moe_plan_workspace_bytes": (_SZ, [_I64, _I32]),
     "art_moe_dispatch_plan": (_I32, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),

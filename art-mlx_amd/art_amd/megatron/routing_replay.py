@@ -1,33 +1,38 @@
-"""MoE routing replay: bundle format, bundle builder and the per-call controller.
+"""MoE routing replay: route bundles, their builder, and the controller that
+feeds each router its replayed top-k ids, device-first.
 
-Host-side counterpart of /root/reference/src/art/megatron/routing_replay.py.
-A *bundle* holds, for every training step, router and router call, the top-k
-expert ids the inference engine chose for each token; the *controller* maps
-the tokens of the local micro-batch (by global token uid) to bundle rows and
-hands the router a ``[T_local, k]`` int64 target that replaces top-k
-selection.  On this build the target feeds ``ops.router_replay`` (the HIP
-gather + softmax kernel) through :class:`RouterReplay` / :class:`TopKRouter`,
-or ``moe_lora_layer(..., target=...)`` directly.
+What is kept from the reference (/root/reference/src/art/megatron/routing_replay.py)
+because it is format or interface:
 
-On-disk format (identical to the reference, routing_replay.py:369-462):
-  manifest.json            format_version "moe_routing_replay_v2", topology,
-                           num_steps, max_topk, router_keys, steps{step: {file,
-                           routers{router_key: {call: {num_experts, sample_index?,
-                           micro_slot?, rank_token_counts?}}}}}
-  step_%06d.safetensors    "global_token_uids" int64 [N] and, per call,
-                           "{router_key}/call_{i}/expert_indices" int32 [N,k],
-                           ".../expert_probs" fp32 [N,k] (optional),
-                           ".../expert_mask" bool [N,k]
+* the on-disk bundle ``moe_routing_replay_v2``: ``manifest.json`` plus one
+  ``step_%06d.safetensors`` per step holding ``global_token_uids`` and
+  ``<router key>/call_<i>/expert_indices|expert_mask[|expert_probs]``
+  (:288-462), and router keys ``chunk_CC.layer_LLLL.mlp.router`` (:89-115);
+* the public classes and the controller methods a trainer calls
+  (``install_router_patches``, ``set_step``, ``begin_micro``,
+  ``set_local_input_token_uids`` / ``prepare_micro_targets``,
+  ``set_active_token_uid_key``, ``finalize_step``, ...), the megatron
+  ``RouterReplay`` driving contract (:1388-1435) and the error fragments the
+  reference's tests match (tests/unit/test_moe_routing_replay.py:439-524);
+* the synthetic-route seeds: ``random.Random(seed + (pos+1)*1_299_709)
+  .sample(range(E), k)`` with seed ``(sample+1)*1_000_003 + (layer+1)*97_003``
+  for captured sequences, ``+ (slot+1)*9_176`` with the step in place of the
+  sample for padded micro slots, and ``(step+1)*1_000_003 + (call+1)*97_003``
+  for tokens staged without a uid (:538-555, 594-610, 1471-1472).
 
-Synthetic rows (tokens with no captured route) use Python's stdlib
-``random.Random(seed + (pos + 1) * 1_299_709).sample(range(E), k)`` with the
-reference's seed formulas (routing_replay.py:538-539, 553-555, 594-610,
-1467-1472), so bundles and targets built here match the reference's bit for
-bit.
-
-Parallel topology enters only through a ``parallel_state``-like object
-(tensor/context/data-parallel world sizes and ranks); the default is a single
-process (all sizes 1), which is what one GPU runs.
+How it works here.  A step's routes are validated once at ``set_step`` and,
+on a GPU, every call this rank will consume is copied into ONE device route
+table (all routers and calls back to back, a single pinned host-to-device
+copy on a side stream).  A micro's token uids are turned into step rows by a
+vectorised uid index (dense offset or sorted lookup) once per uid layout;
+that int32 row map is uploaded once and shared by every router, and each
+router call's target is a view ``(table[call rows], row map)`` that the HIP
+replay kernel reads directly (``ops.router_replay_rows``).  Tokens without a
+uid (negative uids) get synthetic rows in a small per-call side table that
+the row map addresses with negative entries.  On the CPU, or with
+``device_targets=False``, targets are plain ``[T, k]`` int64 tensors (what
+megatron's own RouterReplay consumes).  Call consumption per router is a
+small cursor state machine that also recognises activation-recompute calls.
 """
 from __future__ import annotations
 
@@ -40,98 +45,90 @@ import random
 import re
 import types
 import weakref
-from collections import defaultdict
-from dataclasses import dataclass
+from collections.abc import Iterable, Mapping
+from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Any, Callable, Iterable, Mapping
+from typing import Any, Callable
 
 import torch
+
+logger = logging.getLogger(__name__)
 
 ROUTER_NAME_TOKEN = ".mlp.router"
 ROUTER_KEY_FORMAT_VERSION = "moe_routing_replay_v2"
 GLOBAL_TOKEN_UIDS_KEY = "global_token_uids"
 
-# seed constants of the synthetic-row generator (routing_replay.py:538-539, 553-555, 605, 1471)
+# seed formula of the synthetic routes (a data-format contract)
 _SEED_SAMPLE = 1_000_003
 _SEED_LAYER = 97_003
 _SEED_SLOT = 9_176
 _SEED_POSITION = 1_299_709
 
-_LAYER_RE = re.compile(r"decoder\.layers\.(?P<layer>\d+)\.mlp\.router$")
-_CHUNK_RE = re.compile(r"^chunk(?P<chunk>\d+)\.(?P<name>.+)$")
-logger = logging.getLogger(__name__)
+_LAYER_PATH = re.compile(r"decoder\.layers\.(?P<layer>\d+)\.mlp\.router$")
+_TRACE_PREFIX = re.compile(r"^chunk(?P<chunk>\d+)\.(?P<name>.+)$")
 
-_active_controller: "MoeRoutingReplayController | None" = None
+_installed: "weakref.ReferenceType[MoeRoutingReplayController] | None" = None
 
 
 def active_routing_replay_controller() -> "MoeRoutingReplayController | None":
-    """The controller whose router patches are installed, if any."""
-    return _active_controller
+    """The controller whose router patches are currently installed, if any."""
+    return _installed() if _installed is not None else None
 
 
-# --------------------------------------------------------------------- names
-_FUSED_PAIRS = {"linear_proj", "linear_qkv", "in_proj", "linear_fc1", "linear_fc2"}
+# ----------------------------------------------------------------- router keys
+_DOUBLED = frozenset({"linear_proj", "linear_qkv", "in_proj", "linear_fc1", "linear_fc2"})
 
 
 def canonical_module_name(name: str) -> str:
-    """Drop wrapper segments from a module path: leading ``module.``, every
-    ``_orig_mod`` (torch.compile), doubled fused-linear names and the
-    row-parallel LoRA wrapper (param_name_canonicalization.py:17-54)."""
-    parts = name.split(".")
-    while parts and parts[0] == "module":
-        parts.pop(0)
+    """A module path without wrapper segments: leading ``module.``, every
+    ``_orig_mod`` (torch.compile), a fused linear named twice in a row, and
+    the LoRA wrappers around an output projection
+    (weights/param_name_canonicalization.py:17-54)."""
     out: list[str] = []
-    i = 0
-    while i < len(parts):
-        cur = parts[i]
-        nxt = parts[i + 1] if i + 1 < len(parts) else None
-        if cur == "_orig_mod":
-            i += 1
-        elif nxt is not None and cur in _FUSED_PAIRS and nxt == cur:
-            out.append(cur)
-            i += 2
-        elif nxt == "linear_proj" and cur == "out_proj":
-            out.append(cur)
-            i += 2
-        elif nxt == "linear_proj" and cur == "row_parallel_lora":
-            i += 2
-        else:
-            out.append(cur)
-            i += 1
+    for part in name.split("."):
+        if part == "_orig_mod" or (part == "module" and not out):
+            continue
+        prev = out[-1] if out else None
+        if part in _DOUBLED and prev == part:
+            continue                        # linear_fc1.linear_fc1 -> linear_fc1
+        if part == "linear_proj" and prev == "out_proj":
+            continue                        # out_proj.linear_proj -> out_proj
+        if part == "linear_proj" and prev == "row_parallel_lora":
+            out.pop()                       # row_parallel_lora.linear_proj -> (nothing)
+            continue
+        out.append(part)
     return ".".join(out)
 
 
 def build_router_key_from_module_name(*, chunk_index: int, module_name: str) -> str:
-    """``chunk_{cc}.layer_{llll}.mlp.router`` (routing_replay.py:89-100)."""
-    canonical = canonical_module_name(module_name)
-    m = _LAYER_RE.search(canonical)
-    if m is None:
-        raise RuntimeError(
-            f"Unable to derive router key from module name '{module_name}'. "
-            f"Canonicalized to '{canonical}', expected suffix matching '{_LAYER_RE.pattern}'.")
-    return f"chunk_{chunk_index:02d}.layer_{int(m.group('layer')):04d}.mlp.router"
+    """``chunk_CC.layer_LLLL.mlp.router`` of a router module path."""
+    clean = canonical_module_name(module_name)
+    found = _LAYER_PATH.search(clean)
+    if found is None:
+        raise RuntimeError(f"Unable to derive router key from module name '{module_name}' "
+                           f"(as '{clean}'): it must end in 'decoder.layers.<n>.mlp.router'")
+    return f"chunk_{chunk_index:02d}.layer_{int(found['layer']):04d}.mlp.router"
 
 
 def build_router_key_from_trace_name(trace_module_name: str) -> str:
-    """Router key from a ``chunk<idx>.<module name>`` trace name (routing_replay.py:103-115)."""
-    m = _CHUNK_RE.match(trace_module_name)
-    if m is None:
-        raise RuntimeError("Forward trace router module name must start with 'chunk<idx>.'; "
-                           f"got '{trace_module_name}'")
-    return build_router_key_from_module_name(chunk_index=int(m.group("chunk")),
-                                             module_name=m.group("name"))
+    """Router key of a forward-trace name ``chunk<idx>.<module path>``."""
+    found = _TRACE_PREFIX.match(trace_module_name)
+    if found is None:
+        raise RuntimeError(f"trace name '{trace_module_name}' does not start with 'chunk<idx>.'")
+    return build_router_key_from_module_name(chunk_index=int(found["chunk"]),
+                                             module_name=found["name"])
 
 
-# -------------------------------------------------------------- bundle types
-def _cpu(t: Any, dtype: torch.dtype) -> torch.Tensor:
+# ---------------------------------------------------------------- bundle types
+def _host(t: Any, dtype: torch.dtype, what: str) -> torch.Tensor:
     if not isinstance(t, torch.Tensor):
-        raise TypeError(f"Expected torch.Tensor, got {type(t)}")
+        raise TypeError(f"{what} must be a torch.Tensor, got {type(t).__name__}")
     return t.detach().to(device="cpu", dtype=dtype).contiguous()
 
 
 @dataclass
 class ParallelTopology:
-    """Parallel layout the routes were captured under (routing_replay.py:118-126)."""
+    """Parallel layout the routes were captured under (manifest ``topology``)."""
     tp: int
     ep: int
     etp: int = 1
@@ -147,28 +144,32 @@ class ParallelTopology:
 
     @classmethod
     def from_json(cls, d: Mapping[str, Any]) -> "ParallelTopology":
-        fields = ("tp", "ep", "etp", "dp", "sp", "cp", "pp", "vpp")
-        return cls(**{k: d[k] for k in fields if k in d})
+        return cls(**{k: (bool(v) if k == "sp" else int(v)) for k, v in d.items()})
 
 
 def parallel_topology_from_env() -> ParallelTopology:
-    """Topology from the ART_MEGATRON_* environment (routing_replay.py:577-587)."""
-    def env(name: str, default: int) -> int:
-        raw = os.environ.get(name)
-        return default if raw in (None, "") else int(raw)
-    tp = env("ART_MEGATRON_TENSOR_MODEL_PARALLEL_SIZE", 1)
-    etp = env("ART_MEGATRON_EXPERT_TENSOR_PARALLEL_SIZE",
-              env("ART_MEGATRON_EXPERT_TENSOR_MODEL_PARALLEL_SIZE", 1))
-    return ParallelTopology(tp=tp, ep=env("ART_MEGATRON_EXPERT_MODEL_PARALLEL_SIZE", 1), etp=etp,
-                            dp=1, sp=tp > 1, cp=env("ART_MEGATRON_CONTEXT_PARALLEL_SIZE", 1),
-                            pp=env("ART_MEGATRON_PIPELINE_MODEL_PARALLEL_SIZE", 1))
+    """The topology the ART_MEGATRON_* environment describes (one process)."""
+    def num(*names: str) -> int:
+        for n in names:
+            v = os.environ.get(n)
+            if v:
+                return int(v)
+        return 1
+    tp = num("ART_MEGATRON_TENSOR_MODEL_PARALLEL_SIZE")
+    return ParallelTopology(
+        tp=tp, ep=num("ART_MEGATRON_EXPERT_MODEL_PARALLEL_SIZE"),
+        etp=num("ART_MEGATRON_EXPERT_TENSOR_PARALLEL_SIZE",
+                "ART_MEGATRON_EXPERT_TENSOR_MODEL_PARALLEL_SIZE"),
+        dp=1, sp=tp > 1, cp=num("ART_MEGATRON_CONTEXT_PARALLEL_SIZE"),
+        pp=num("ART_MEGATRON_PIPELINE_MODEL_PARALLEL_SIZE"))
 
 
 @dataclass
 class RouterCallRoute:
-    """Routes of one router call: int32 ids [N,k], optional fp32 probs, bool
-    mask (must be all true), and the micro-batch it belongs to
-    (routing_replay.py:125-218)."""
+    """Captured top-k ids of one router call: ``expert_indices`` int32
+    [tokens, k] (every slot valid: ``expert_mask`` all true), optional
+    ``expert_probs``; ``sample_index`` / ``micro_slot`` say which micro it
+    belongs to (neither: the legacy call-order layout)."""
     expert_indices: torch.Tensor
     expert_mask: torch.Tensor
     num_experts: int
@@ -178,41 +179,34 @@ class RouterCallRoute:
     rank_token_counts: tuple[int, ...] | None = None
 
     def __post_init__(self) -> None:
-        self.expert_indices = _cpu(self.expert_indices, torch.int32)
+        self.expert_indices = _host(self.expert_indices, torch.int32, "expert_indices")
+        self.expert_mask = _host(self.expert_mask, torch.bool, "expert_mask")
         if self.expert_probs is not None:
-            self.expert_probs = _cpu(self.expert_probs, torch.float32)
-        self.expert_mask = _cpu(self.expert_mask, torch.bool)
-        idx = self.expert_indices
-        if idx.ndim != 2:
-            raise RuntimeError(
-                f"expert_indices must have shape [num_tokens, topk], got {tuple(idx.shape)}")
-        if self.expert_probs is not None and self.expert_probs.shape != idx.shape:
-            raise RuntimeError("expert_probs shape must match expert_indices shape, got "
-                               f"{tuple(self.expert_probs.shape)} vs {tuple(idx.shape)}")
-        if self.expert_mask.shape != idx.shape:
-            raise RuntimeError("expert_mask shape must match expert_indices shape, got "
-                               f"{tuple(self.expert_mask.shape)} vs {tuple(idx.shape)}")
+            self.expert_probs = _host(self.expert_probs, torch.float32, "expert_probs")
+        shape = tuple(self.expert_indices.shape)
+        if len(shape) != 2:
+            raise RuntimeError(f"expert_indices is [tokens, topk], got shape {shape}")
+        for name, t in (("expert_mask", self.expert_mask), ("expert_probs", self.expert_probs)):
+            if t is not None and tuple(t.shape) != shape:
+                raise RuntimeError(f"{name} has shape {tuple(t.shape)}, expert_indices {shape}")
         if not bool(self.expert_mask.all()):
-            raise RuntimeError(
-                "masked slots are unsupported by Megatron native MoE routing replay; route "
-                "bundles must contain a valid full top-k expert id row for every replayed token")
+            raise RuntimeError("masked slots are unsupported by native MoE routing replay: every "
+                               "replayed token needs a full row of top-k expert ids")
         self.num_experts = int(self.num_experts)
         if self.num_experts <= 0:
-            raise RuntimeError(f"num_experts must be >0, got {self.num_experts}")
-        if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= self.num_experts):
-            raise RuntimeError("expert_indices contain ids outside [0, num_experts): "
-                               f"num_experts={self.num_experts}")
+            raise RuntimeError(f"num_experts must be positive, got {self.num_experts}")
+        if self.expert_indices.numel() and (int(self.expert_indices.min()) < 0 or
+                                            int(self.expert_indices.max()) >= self.num_experts):
+            raise RuntimeError(f"expert_indices hold ids outside [0, {self.num_experts})")
         if self.sample_index is not None:
             self.sample_index = int(self.sample_index)
         if self.micro_slot is not None:
             self.micro_slot = int(self.micro_slot)
         if self.rank_token_counts is not None:
             counts = tuple(int(c) for c in self.rank_token_counts)
-            if any(c < 0 for c in counts):
-                raise RuntimeError(f"rank_token_counts must be non-negative, got {counts}")
-            if sum(counts) != idx.shape[0]:
-                raise RuntimeError("rank_token_counts must sum to route token count: "
-                                   f"counts={counts}, tokens={idx.shape[0]}")
+            if min(counts, default=0) < 0 or sum(counts) != shape[0]:
+                raise RuntimeError(f"rank_token_counts {counts} must be non-negative and sum to "
+                                   f"the {shape[0]} route tokens")
             self.rank_token_counts = counts
 
     @property
@@ -225,7 +219,7 @@ class RouterCallRoute:
 
     @property
     def call_key(self) -> tuple[str, int] | None:
-        """Which micro-batch the call belongs to: a sample, a dummy micro slot, or unknown."""
+        """Which micro the call belongs to: ("sample", i), ("dummy_micro_slot", j) or None."""
         if self.sample_index is not None:
             return ("sample", self.sample_index)
         if self.micro_slot is not None:
@@ -239,60 +233,49 @@ class StepRouterRoutes:
 
     def __post_init__(self) -> None:
         if not self.calls:
-            raise RuntimeError("StepRouterRoutes.calls cannot be empty")
-        for ci in self.calls:
-            if ci < 0:
-                raise RuntimeError(f"call_index must be >=0, got {ci}")
+            raise RuntimeError("a router needs at least one call per step")
+        if min(self.calls) < 0:
+            raise RuntimeError(f"call indices must be >= 0, got {sorted(self.calls)}")
 
 
 @dataclass
 class StepRoutes:
-    """All routers of one step plus the step's global token uids (routing_replay.py:221-285)."""
     routers: dict[str, StepRouterRoutes]
     global_token_uids: torch.Tensor
 
     def __post_init__(self) -> None:
         if not self.routers:
-            raise RuntimeError("StepRoutes.routers cannot be empty")
-        uids = _cpu(self.global_token_uids, torch.int64)
-        self.global_token_uids = uids
-        if uids.ndim != 1:
-            raise RuntimeError("global_token_uids must have shape [num_global_tokens], got "
-                               f"{tuple(uids.shape)}")
+            raise RuntimeError("a step needs at least one router")
+        uids = _host(self.global_token_uids, torch.int64, "global_token_uids")
+        if uids.dim() != 1:
+            raise RuntimeError(f"global_token_uids is [tokens], got shape {tuple(uids.shape)}")
         if torch.unique(uids).numel() != uids.numel():
             raise RuntimeError("global_token_uids must be unique per step")
+        self.global_token_uids = uids
         n = uids.numel()
         per_micro: dict[tuple[str, int], int] = {}
         for rk, rr in self.routers.items():
             for ci, route in rr.calls.items():
-                key = route.call_key
-                tokens = route.num_global_tokens
+                key, rows = route.call_key, route.num_global_tokens
+                if key is None and rows != n:
+                    raise RuntimeError(f"router '{rk}' call {ci}: {rows} route rows must match step "
+                                       f"global_token_uids ({n}) without per-micro metadata")
                 if key is None:
-                    if tokens != n:
-                        raise RuntimeError(
-                            "Route token count must match step global_token_uids when no "
-                            f"per-micro metadata is present: router='{rk}', call={ci}, "
-                            f"route_tokens={tokens}, global_token_uids={n}")
                     continue
-                if tokens > n:
-                    raise RuntimeError(
-                        "Route token count exceeds step global_token_uids span: "
-                        f"router='{rk}', call={ci}, call_key={key}, route_tokens={tokens}, "
-                        f"global_token_uids={n}")
-                seen = per_micro.setdefault(key, tokens)
-                if seen != tokens:
-                    raise RuntimeError(
-                        "Route token count must be consistent for the same micro: "
-                        f"router='{rk}', call={ci}, call_key={key}, expected={seen}, got={tokens}")
+                if rows > n:
+                    raise RuntimeError(f"router '{rk}' call {ci}: {rows} route rows exceed the "
+                                       f"step's {n} global_token_uids")
+                if per_micro.setdefault(key, rows) != rows:
+                    raise RuntimeError(f"router '{rk}' call {ci}: micro {key} has {rows} route "
+                                       f"rows here and {per_micro[key]} elsewhere")
 
 
-def _key(router_key: str, call_index: int, name: str) -> str:
+def _tensor_key(router_key: str, call_index: int, name: str) -> str:
     return f"{router_key}/call_{call_index}/{name}"
 
 
 @dataclass
 class MoeRoutingReplayBundle:
-    """Routes for ``num_steps`` steps (routing_replay.py:288-462)."""
     topology: ParallelTopology
     num_steps: int
     max_topk: int
@@ -302,235 +285,219 @@ class MoeRoutingReplayBundle:
 
     def __post_init__(self) -> None:
         if self.format_version != ROUTER_KEY_FORMAT_VERSION:
-            raise RuntimeError(f"Unsupported MoE routing replay bundle format: "
-                               f"{self.format_version!r}; expected {ROUTER_KEY_FORMAT_VERSION!r}")
-        if self.num_steps <= 0:
-            raise RuntimeError(f"num_steps must be >0, got {self.num_steps}")
-        if self.max_topk <= 0:
-            raise RuntimeError(f"max_topk must be >0, got {self.max_topk}")
-        if not self.router_keys:
-            raise RuntimeError("router_keys cannot be empty")
-        if len(set(self.router_keys)) != len(self.router_keys):
-            raise RuntimeError("router_keys must be unique")
-        want = set(range(self.num_steps))
-        if set(self.steps) != want:
-            raise RuntimeError(f"steps must contain exactly {sorted(want)}, got {sorted(self.steps)}")
-        keys = set(self.router_keys)
-        for si, sr in self.steps.items():
-            if set(sr.routers) != keys:
-                raise RuntimeError(f"Step {si} router keys differ from bundle router keys: "
-                                   f"step_keys={sorted(sr.routers)}, router_keys={self.router_keys}")
-            for rr in sr.routers.values():
+            raise RuntimeError(f"bundle format {self.format_version!r} is not "
+                               f"{ROUTER_KEY_FORMAT_VERSION!r}")
+        if self.num_steps <= 0 or self.max_topk <= 0:
+            raise RuntimeError(f"num_steps ({self.num_steps}) and max_topk ({self.max_topk}) "
+                               "must be positive")
+        keys = list(self.router_keys)
+        if not keys or len(set(keys)) != len(keys):
+            raise RuntimeError(f"router_keys must be non-empty and unique, got {keys}")
+        if set(self.steps) != set(range(self.num_steps)):
+            raise RuntimeError(f"steps must contain exactly 0..{self.num_steps - 1}, "
+                               f"got {sorted(self.steps)}")
+        for si, step in self.steps.items():
+            if set(step.routers) != set(keys):
+                raise RuntimeError(f"step {si} has routers {sorted(step.routers)}, the bundle "
+                                   f"{sorted(keys)}")
+            for rr in step.routers.values():
                 for route in rr.calls.values():
                     if route.max_topk > self.max_topk:
-                        raise RuntimeError("Route topk exceeds bundle max_topk: "
-                                           f"route_topk={route.max_topk}, max_topk={self.max_topk}")
+                        raise RuntimeError(f"a route's topk {route.max_topk} exceeds bundle "
+                                           f"max_topk {self.max_topk}")
 
-    # ------------------------------------------------------------ disk I/O
-    @classmethod
-    def from_dir(cls, bundle_dir: str | Path) -> "MoeRoutingReplayBundle":
-        from safetensors.torch import load_file
-
-        base = Path(bundle_dir)
-        mpath = base / "manifest.json"
-        if not mpath.exists():
-            raise FileNotFoundError(f"Missing routing replay manifest: {mpath}")
-        manifest = json.loads(mpath.read_text(encoding="utf-8"))
-        if manifest.get("format_version") != ROUTER_KEY_FORMAT_VERSION:
-            raise RuntimeError(f"Unsupported MoE routing replay bundle format: "
-                               f"{manifest.get('format_version')!r}; expected "
-                               f"{ROUTER_KEY_FORMAT_VERSION!r}")
-        steps: dict[int, StepRoutes] = {}
-        for step_str, info in manifest["steps"].items():
-            si = int(step_str)
-            # clone: own the storage instead of keeping the file mapped
-            tensors = {k: v.clone().contiguous() for k, v in load_file(str(base / info["file"])).items()}
-            if GLOBAL_TOKEN_UIDS_KEY not in tensors:
-                raise RuntimeError(f"Missing tensor key '{GLOBAL_TOKEN_UIDS_KEY}' for step={si}")
-            routers: dict[str, StepRouterRoutes] = {}
-            for rk, calls_info in info["routers"].items():
-                calls: dict[int, RouterCallRoute] = {}
-                for ci_str, ci_info in calls_info.items():
-                    ci = int(ci_str)
-                    need = [_key(rk, ci, "expert_indices"), _key(rk, ci, "expert_mask")]
-                    missing = [k for k in need if k not in tensors]
-                    if missing:
-                        raise RuntimeError(f"Missing tensor keys {missing} in {info['file']}")
-                    calls[ci] = RouterCallRoute(
-                        expert_indices=tensors[need[0]], expert_mask=tensors[need[1]],
-                        expert_probs=tensors.get(_key(rk, ci, "expert_probs")),
-                        num_experts=int(ci_info["num_experts"]),
-                        sample_index=ci_info.get("sample_index"),
-                        micro_slot=ci_info.get("micro_slot"),
-                        rank_token_counts=ci_info.get("rank_token_counts"))
-                routers[rk] = StepRouterRoutes(calls=calls)
-            steps[si] = StepRoutes(routers=routers, global_token_uids=tensors[GLOBAL_TOKEN_UIDS_KEY])
-        return cls(format_version=manifest["format_version"],
-                   topology=ParallelTopology.from_json(manifest["topology"]),
-                   num_steps=int(manifest["num_steps"]), max_topk=int(manifest["max_topk"]),
-                   router_keys=list(manifest["router_keys"]), steps=steps)
-
+    # -------------------------------------------------------------- on disk
     def to_dir(self, bundle_dir: str | Path) -> None:
         from safetensors.torch import save_file
-
         base = Path(bundle_dir)
         base.mkdir(parents=True, exist_ok=True)
         steps_manifest: dict[str, Any] = {}
         for si in sorted(self.steps):
-            sr = self.steps[si]
-            if si < 0:
-                raise ValueError(f"step_index must be non-negative, got {si}")
-            fname = f"step_{si:06d}.safetensors"
-            tensors: dict[str, torch.Tensor] = {GLOBAL_TOKEN_UIDS_KEY: sr.global_token_uids}
-            routers_manifest: dict[str, Any] = {}
-            for rk in sorted(sr.routers):
-                calls_manifest: dict[str, Any] = {}
-                for ci in sorted(sr.routers[rk].calls):
-                    route = sr.routers[rk].calls[ci]
-                    tensors[_key(rk, ci, "expert_indices")] = route.expert_indices
+            step = self.steps[si]
+            tensors = {GLOBAL_TOKEN_UIDS_KEY: step.global_token_uids}
+            routers: dict[str, Any] = {}
+            for rk in sorted(step.routers):
+                calls: dict[str, Any] = {}
+                for ci in sorted(step.routers[rk].calls):
+                    route = step.routers[rk].calls[ci]
+                    tensors[_tensor_key(rk, ci, "expert_indices")] = route.expert_indices
+                    tensors[_tensor_key(rk, ci, "expert_mask")] = route.expert_mask
                     if route.expert_probs is not None:
-                        tensors[_key(rk, ci, "expert_probs")] = route.expert_probs
-                    tensors[_key(rk, ci, "expert_mask")] = route.expert_mask
-                    meta: dict[str, Any] = {"num_experts": route.num_experts}
-                    if route.sample_index is not None:
-                        meta["sample_index"] = route.sample_index
-                    if route.micro_slot is not None:
-                        meta["micro_slot"] = route.micro_slot
+                        tensors[_tensor_key(rk, ci, "expert_probs")] = route.expert_probs
+                    info: dict[str, Any] = {"num_experts": route.num_experts}
+                    for name in ("sample_index", "micro_slot"):
+                        if getattr(route, name) is not None:
+                            info[name] = getattr(route, name)
                     if route.rank_token_counts is not None:
-                        meta["rank_token_counts"] = list(route.rank_token_counts)
-                    calls_manifest[str(ci)] = meta
-                routers_manifest[rk] = calls_manifest
+                        info["rank_token_counts"] = list(route.rank_token_counts)
+                    calls[str(ci)] = info
+                routers[rk] = calls
+            fname = f"step_{si:06d}.safetensors"
             save_file(tensors, str(base / fname))
-            steps_manifest[str(si)] = {"file": fname, "routers": routers_manifest}
+            steps_manifest[str(si)] = {"file": fname, "routers": routers}
         manifest = {"format_version": self.format_version, "topology": self.topology.to_json(),
                     "num_steps": self.num_steps, "max_topk": self.max_topk,
-                    "router_keys": self.router_keys, "steps": steps_manifest}
+                    "router_keys": list(self.router_keys), "steps": steps_manifest}
         (base / "manifest.json").write_text(json.dumps(manifest, indent=2, sort_keys=True),
                                             encoding="utf-8")
 
+    @classmethod
+    def from_dir(cls, bundle_dir: str | Path) -> "MoeRoutingReplayBundle":
+        from safetensors.torch import load_file
+        base = Path(bundle_dir)
+        mpath = base / "manifest.json"
+        if not mpath.exists():
+            raise FileNotFoundError(f"no routing replay manifest at {mpath}")
+        manifest = json.loads(mpath.read_text(encoding="utf-8"))
+        if manifest.get("format_version") != ROUTER_KEY_FORMAT_VERSION:
+            raise RuntimeError(f"bundle format {manifest.get('format_version')!r} is not "
+                               f"{ROUTER_KEY_FORMAT_VERSION!r}")
+        steps: dict[int, StepRoutes] = {}
+        for si, sinfo in manifest["steps"].items():
+            # clone: the loaded tensors may map the file, which must not stay
+            # open (shared-filesystem cleanup) while a long-lived rank holds them
+            raw = {k: v.clone() for k, v in load_file(str(base / sinfo["file"])).items()}
+            if GLOBAL_TOKEN_UIDS_KEY not in raw:
+                raise RuntimeError(f"{sinfo['file']} lacks '{GLOBAL_TOKEN_UIDS_KEY}'")
+            routers: dict[str, StepRouterRoutes] = {}
+            for rk, cinfo in sinfo["routers"].items():
+                calls: dict[int, RouterCallRoute] = {}
+                for ci_s, info in cinfo.items():
+                    ci = int(ci_s)
+                    need = [_tensor_key(rk, ci, n) for n in ("expert_indices", "expert_mask")]
+                    absent = [k for k in need if k not in raw]
+                    if absent:
+                        raise RuntimeError(f"{sinfo['file']} lacks {absent}")
+                    calls[ci] = RouterCallRoute(
+                        expert_indices=raw[need[0]], expert_mask=raw[need[1]],
+                        expert_probs=raw.get(_tensor_key(rk, ci, "expert_probs")),
+                        num_experts=int(info["num_experts"]), sample_index=info.get("sample_index"),
+                        micro_slot=info.get("micro_slot"),
+                        rank_token_counts=info.get("rank_token_counts"))
+                routers[rk] = StepRouterRoutes(calls=calls)
+            steps[int(si)] = StepRoutes(routers=routers, global_token_uids=raw[GLOBAL_TOKEN_UIDS_KEY])
+        return cls(topology=ParallelTopology.from_json(manifest["topology"]),
+                   num_steps=int(manifest["num_steps"]), max_topk=int(manifest["max_topk"]),
+                   router_keys=list(manifest["router_keys"]), steps=steps,
+                   format_version=manifest["format_version"])
 
-# ------------------------------------------------------------ synthetic rows
+
+# ---------------------------------------------------------- synthetic routes
 def synthetic_replay_rows(*, row_positions: torch.Tensor | Iterable[int], num_experts: int,
                           topk: int, dtype: torch.dtype, seed: int) -> torch.Tensor:
-    """k distinct expert ids per position, ``random.Random(seed + (pos+1)*1_299_709)
-    .sample(range(E), k)`` (routing_replay.py:594-610)."""
-    pos = row_positions.tolist() if isinstance(row_positions, torch.Tensor) else list(row_positions)
-    rows = [random.Random(seed + (int(p) + 1) * _SEED_POSITION).sample(range(num_experts), topk)
-            for p in pos]
-    if not rows:
-        return torch.empty((0, topk), dtype=dtype)
-    return torch.tensor(rows, dtype=dtype)
-
-
-_synthetic_replay_rows = synthetic_replay_rows
-
-
-# ------------------------------------------------------------------ builder
-def _rows_without_future_scored_tokens(group_ids: torch.Tensor, parent_ids: torch.Tensor,
-                                       logprobs: torch.Tensor) -> torch.Tensor:
-    """Branch rows after which no token of the same group is scored: their
-    route cannot influence a trained token (routing_replay.py:38-68)."""
-    valid = group_ids != -1
-    branch = valid & (group_ids != parent_ids)
-    scored = valid & torch.isfinite(logprobs)
-    out = torch.zeros_like(branch)
-    g = group_ids.tolist()
-    br = branch.tolist()
-    sc = scored.tolist()
-    for s in range(len(g)):
-        scored_later: set[int] = set()
-        for p in range(len(g[s]) - 1, -1, -1):
-            gid = g[s][p]
-            if gid == -1:
-                continue
-            out[s, p] = br[s][p] and gid not in scored_later
-            if sc[s][p]:
-                scored_later.add(gid)
+    """[len(positions), topk] distinct expert ids per position from Python's
+    ``random.Random(seed + (position + 1) * 1_299_709).sample(range(E), k)``:
+    routes for tokens that have none, reproducible from (seed, position)."""
+    positions = row_positions.tolist() if isinstance(row_positions, torch.Tensor) \
+        else list(row_positions)
+    experts = range(num_experts)
+    out = torch.empty((len(positions), topk), dtype=dtype)
+    for i, pos in enumerate(positions):
+        out[i] = torch.tensor(random.Random(seed + (int(pos) + 1) * _SEED_POSITION)
+                              .sample(experts, topk), dtype=dtype)
     return out
+
+
+# ------------------------------------------------------------------- builder
+def _route_free_rows(group_ids: torch.Tensor, parent_ids: torch.Tensor,
+                     logprobs: torch.Tensor) -> torch.Tensor:
+    """Rows whose missing route cannot matter, [S, seq] bool: terminal
+    completion tokens (a branch row whose next row starts another group) and
+    branch rows after which no token of the same group is scored (vLLM ran
+    no forward for a sequence's last token; prefix-tree packing may leave a
+    masked suffix in the branch).  The second set is found in one pass: a
+    row p of group g is free if g's last scored row is not after p."""
+    real = group_ids != -1
+    branch = real & (group_ids != parent_ids)
+    following = torch.nn.functional.pad(group_ids[:, 1:], (0, 1), value=-1)
+    terminal = branch & (group_ids != following)
+    scored = real & torch.isfinite(logprobs)
+    seq = group_ids.shape[1]
+    pos = torch.arange(seq).expand_as(group_ids)
+    gid = torch.where(real, group_ids, 0).long()
+    span = int(gid.max()) + 1 if gid.numel() else 1
+    last_scored = torch.full((group_ids.shape[0], span), -1, dtype=torch.long)
+    last_scored.scatter_reduce_(1, gid, torch.where(scored, pos, -1), reduce="amax")
+    no_later_score = last_scored.gather(1, gid) <= pos
+    return terminal | (branch & no_later_score)
 
 
 def build_moe_routing_replay_bundle_from_packed_tensors(
         *, packed_tensors: Mapping[str, Any], global_grad_accumulation_sequences: int,
         topology: ParallelTopology | None = None) -> MoeRoutingReplayBundle:
-    """One step per ``global_grad_accumulation_sequences`` packed sequences, one
-    router key per layer, one call per sequence (routing_replay.py:465-574).
+    """A bundle with one step per ``global_grad_accumulation_sequences``
+    packed sequences, one router per MoE layer and one call per sequence
+    (the micro of its sample); step slots past the last sequence become
+    padded micro slots of synthetic routes.
 
-    ``packed_tensors["moe_routing_replay"]`` carries ``expert_indices``
-    [S, seq, L, k], ``token_mask`` [S, seq] (route captured) and ``num_experts``;
-    ``group_ids``, ``parent_ids`` and ``logprobs`` [S, seq] decide which missing
-    routes are tolerated (padding, terminal completion tokens, branch tails
-    with no later scored token) and get synthetic rows.  Step slots past the
-    last sequence become dummy micro slots with synthetic routes.
+    ``packed_tensors["moe_routing_replay"]`` has ``expert_indices`` [S, seq,
+    L, k], ``token_mask`` [S, seq] (route captured) and ``num_experts``;
+    ``group_ids`` / ``parent_ids`` / ``logprobs`` [S, seq] decide which
+    uncaptured rows are acceptable (padding and the rows of
+    ``_route_free_rows``) and get synthetic routes.
     """
     rr = packed_tensors.get("moe_routing_replay")
     if rr is None:
         raise RuntimeError("Packed tensors do not contain MoE routing replay data")
-    if global_grad_accumulation_sequences <= 0:
-        raise RuntimeError("global_grad_accumulation_sequences must be positive when building MoE "
-                           f"routing replay bundles, got {global_grad_accumulation_sequences}")
-    idx = rr.expert_indices
-    token_mask = rr.token_mask
-    n_seq, seq_len, n_layers, topk = (int(d) for d in idx.shape)
-    n_exp = int(rr.num_experts)
-    gid = packed_tensors["group_ids"]
-    pid = packed_tensors["parent_ids"]
-    valid = gid != -1
-    next_gid = torch.cat([gid[:, 1:], torch.full_like(gid[:, :1], -1)], dim=1)
-    terminal = valid & (gid != pid) & (gid != next_gid)
-    tolerated = terminal | _rows_without_future_scored_tokens(gid, pid, packed_tensors["logprobs"])
-    bad = valid & ~token_mask & ~tolerated
+    per_step = int(global_grad_accumulation_sequences)
+    if per_step <= 0:
+        raise RuntimeError(f"global_grad_accumulation_sequences must be positive, got {per_step}")
+    ids = rr.expert_indices
+    captured = rr.token_mask.bool()
+    n_seq, seq, n_layers, k = (int(d) for d in ids.shape)
+    e = int(rr.num_experts)
+    gids = packed_tensors["group_ids"]
+    bad = (gids != -1) & ~captured & ~_route_free_rows(gids, packed_tensors["parent_ids"],
+                                                       packed_tensors["logprobs"])
     if bool(bad.any()):
         raise RuntimeError("Packed tensors are missing MoE routes outside terminal completion "
-                           f"tokens: missing_rows={int(bad.sum())}")
+                           f"tokens ({int(bad.sum())} rows)")
     keys = [f"chunk_00.layer_{layer:04d}.mlp.router" for layer in range(n_layers)]
-    gga = global_grad_accumulation_sequences
-    n_steps = math.ceil(n_seq / gga)
+    n_steps = math.ceil(n_seq / per_step)
     steps: dict[int, StepRoutes] = {}
-    ones = lambda t: torch.ones_like(t, dtype=torch.bool)  # noqa: E731
     for step in range(n_steps):
         routers: dict[str, StepRouterRoutes] = {}
         for layer, rk in enumerate(keys):
             calls: dict[int, RouterCallRoute] = {}
-            for slot in range(gga):
-                sample = step * gga + slot
+            for slot in range(per_step):
+                sample = step * per_step + slot
                 if sample < n_seq:
-                    rows = idx[sample, :, layer, :].clone()
-                    missing = ~token_mask[sample]
-                    if bool(missing.any()):
-                        rows[missing] = synthetic_replay_rows(
-                            row_positions=torch.nonzero(missing).flatten(), num_experts=n_exp,
-                            topk=topk, dtype=idx.dtype,
+                    rows = ids[sample, :, layer, :].to(torch.int32).clone()
+                    holes = torch.nonzero(~captured[sample]).flatten()
+                    if holes.numel():
+                        rows[holes] = synthetic_replay_rows(
+                            row_positions=holes, num_experts=e, topk=k, dtype=torch.int32,
                             seed=(sample + 1) * _SEED_SAMPLE + (layer + 1) * _SEED_LAYER)
-                    calls[slot] = RouterCallRoute(expert_indices=rows, expert_mask=ones(rows),
-                                                  num_experts=n_exp, sample_index=sample)
+                    meta = {"sample_index": sample}
                 else:
                     rows = synthetic_replay_rows(
-                        row_positions=range(seq_len), num_experts=n_exp, topk=topk,
-                        dtype=idx.dtype,
+                        row_positions=range(seq), num_experts=e, topk=k, dtype=torch.int32,
                         seed=(step + 1) * _SEED_SAMPLE + (layer + 1) * _SEED_LAYER
                         + (slot + 1) * _SEED_SLOT)
-                    calls[slot] = RouterCallRoute(expert_indices=rows, expert_mask=ones(rows),
-                                                  num_experts=n_exp, micro_slot=slot)
+                    meta = {"micro_slot": slot}
+                calls[slot] = RouterCallRoute(expert_indices=rows,
+                                              expert_mask=torch.ones_like(rows, dtype=torch.bool),
+                                              num_experts=e, **meta)
             routers[rk] = StepRouterRoutes(calls=calls)
         steps[step] = StepRoutes(routers=routers,
-                                 global_token_uids=torch.arange(seq_len, dtype=torch.int64))
+                                 global_token_uids=torch.arange(seq, dtype=torch.int64))
     return MoeRoutingReplayBundle(topology=topology or parallel_topology_from_env(),
-                                  num_steps=n_steps, max_topk=topk, router_keys=keys, steps=steps)
+                                  num_steps=n_steps, max_topk=k, router_keys=keys, steps=steps)
 
 
-# ---------------------------------------------- device-resident replay target
+# ------------------------------------------------- device replay target type
 class DeviceReplayTarget:
-    """A replay target kept as a device route table and a row map: token t
-    replays ``table[rows[t]]`` (table int32 [N, k], rows int32 [T], both on
-    the device).  The router kernels read it directly
-    (``ops.router_replay_rows``), so a step's table is uploaded once and a
-    micro's row map once for every router, instead of one host-gathered
-    [T, k] target per router call (routing_replay.py:1437-1474, 1530-1572)."""
+    """A replay target in device memory: token t replays ``table[rows[t]]``
+    (rows[t] >= 0) or ``extra[-rows[t] - 1]`` (rows[t] < 0, synthetic rows);
+    table / extra int32 [N, k] / [X, k], rows int32 [T].  The HIP replay
+    kernel reads it as it is (``ops.router_replay_rows``)."""
 
-    def __init__(self, table: torch.Tensor, rows: torch.Tensor) -> None:
-        if table.dim() != 2 or rows.dim() != 1:
-            raise RuntimeError("DeviceReplayTarget needs table [N, k] and rows [T]")
-        self.table, self.rows = table, rows
+    def __init__(self, table: torch.Tensor, rows: torch.Tensor,
+                 extra: torch.Tensor | None = None) -> None:
+        if table.dim() != 2 or rows.dim() != 1 or (extra is not None and extra.dim() != 2):
+            raise RuntimeError("DeviceReplayTarget takes a table [N, k], rows [T] and an "
+                               "optional extra table [X, k]")
+        self.table, self.rows, self.extra = table, rows, extra
 
     @property
     def shape(self) -> torch.Size:
@@ -541,11 +508,16 @@ class DeviceReplayTarget:
         return self.table.device
 
     def materialize(self) -> torch.Tensor:
-        """The [T, k] int64 target (for consumers that need the ids themselves)."""
-        return self.table.index_select(0, self.rows.long()).long()
+        """The [T, k] int64 target ids."""
+        r = self.rows.long()
+        out = self.table.index_select(0, r.clamp_min(0)).long()
+        if self.extra is not None and bool((r < 0).any()):
+            side = self.extra.index_select(0, (-r - 1).clamp(0, self.extra.shape[0] - 1)).long()
+            out = torch.where((r < 0).unsqueeze(1), side, out)
+        return out
 
 
-# ----------------------------------------------------- router replay object
+# -------------------------------------------------- megatron RouterReplay API
 class RouterReplayAction(enum.Enum):
     RECORD = "record"
     REPLAY_FORWARD = "replay_forward"
@@ -553,37 +525,33 @@ class RouterReplayAction(enum.Enum):
 
 
 class RouterReplay:
-    """Per-router replay state with megatron's RouterReplay interface (the
-    contract the controller drives, restated from the fake in
-    tests/unit/test_moe_routing_replay.py:136-161): a target set with
-    ``set_target_indices`` and the REPLAY_FORWARD action replaces top-k."""
+    """Replay state of one router with megatron's ``RouterReplay`` interface:
+    under REPLAY_FORWARD the target set with ``set_target_indices`` replaces
+    the top-k selection.  The class-level calls act on every live instance."""
 
-    _instances: "weakref.WeakSet[RouterReplay]" = weakref.WeakSet()
+    _live: "weakref.WeakSet[RouterReplay]" = weakref.WeakSet()
 
     def __init__(self) -> None:
-        self.target_topk_idx: torch.Tensor | None = None
+        self.target_topk_idx: torch.Tensor | DeviceReplayTarget | None = None
         self.recorded_topk_idx: torch.Tensor | None = None
         self.router_replay_action: RouterReplayAction | None = None
-        RouterReplay._instances.add(self)
+        RouterReplay._live.add(self)
 
-    # class-wide controls
     @staticmethod
     def clear_global_indices() -> None:
-        for r in list(RouterReplay._instances):
+        for r in list(RouterReplay._live):
             r.clear_indices()
 
     @staticmethod
     def set_global_router_replay_action(action: RouterReplayAction) -> None:
-        for r in list(RouterReplay._instances):
+        for r in list(RouterReplay._live):
             r.router_replay_action = action
 
     @staticmethod
     def clear_global_router_replay_action() -> None:
-        for r in list(RouterReplay._instances):
-            r.router_replay_action = None
+        RouterReplay.set_global_router_replay_action(None)
 
-    # per instance
-    def set_target_indices(self, topk_indices: torch.Tensor) -> None:
+    def set_target_indices(self, topk_indices) -> None:
         self.target_topk_idx = topk_indices
 
     def set_router_replay_action(self, action: RouterReplayAction | None) -> None:
@@ -593,8 +561,7 @@ class RouterReplay:
         self.router_replay_action = None
 
     def clear_indices(self) -> None:
-        self.target_topk_idx = None
-        self.recorded_topk_idx = None
+        self.target_topk_idx = self.recorded_topk_idx = None
 
     def record_indices(self, topk_indices: torch.Tensor) -> None:
         self.recorded_topk_idx = topk_indices.detach()
@@ -602,17 +569,16 @@ class RouterReplay:
     def get_recorded_indices(self) -> torch.Tensor | None:
         return self.recorded_topk_idx
 
-    def active_target(self) -> torch.Tensor | None:
-        """The target that replaces top-k now, or None."""
-        if self.router_replay_action == RouterReplayAction.REPLAY_FORWARD:
-            return self.target_topk_idx
-        return None
+    def active_target(self):
+        """The target replacing top-k now (None unless REPLAY_FORWARD)."""
+        return self.target_topk_idx if self.router_replay_action is RouterReplayAction.REPLAY_FORWARD \
+            else None
 
     def get_replay_topk(self, scores: torch.Tensor, topk: int, num_groups: int | None = None,
                         group_topk: int | None = None,
                         default_compute_topk: Callable[..., Any] | None = None):
-        """(selected scores, indices): the target's scores under REPLAY_FORWARD,
-        else the default top-k (recorded under RECORD)."""
+        """(selected scores, ids): the target's under REPLAY_FORWARD, otherwise
+        ``default_compute_topk`` (recorded under RECORD)."""
         target = self.active_target()
         if target is not None:
             if isinstance(target, DeviceReplayTarget):
@@ -620,14 +586,14 @@ class RouterReplay:
             ids = target.to(device=scores.device, dtype=torch.long)
             return scores.gather(1, ids), ids
         vals, ids = default_compute_topk(scores, topk, num_groups, group_topk)
-        if self.router_replay_action == RouterReplayAction.RECORD:
+        if self.router_replay_action is RouterReplayAction.RECORD:
             self.record_indices(ids)
         return vals, ids
 
 
-# ------------------------------------------------------- parallel topology
+# ---------------------------------------------------------- parallel layout
 class SingleProcessParallelState:
-    """The parallel_state the controller consults, for one process on one GPU."""
+    """The parallel_state queries the replay needs, for one process on one GPU."""
 
     def get_tensor_model_parallel_world_size(self) -> int:
         return 1
@@ -638,6 +604,9 @@ class SingleProcessParallelState:
     def get_context_parallel_world_size(self) -> int:
         return 1
 
+    def get_context_parallel_rank(self) -> int:
+        return 0
+
     def get_data_parallel_world_size(self) -> int:
         return 1
 
@@ -646,604 +615,550 @@ class SingleProcessParallelState:
 
 
 class TopologyAwareLocalTokenIndexer:
-    """Local token uid order of this rank: context-parallel slice, then the
-    sequence-parallel slice of merged rows (routing_replay.py:624-683)."""
+    """This rank's token uids of a packed sequence: the context-parallel
+    share (chunks r and 2cp-1-r of 2cp equal chunks, megatron's load-balanced
+    split) and, with sequence parallelism, the tensor-parallel rank's slice."""
 
     def __init__(self, parallel_state_module: Any | None = None) -> None:
         self._ps = parallel_state_module or SingleProcessParallelState()
 
     def build_local_token_uids(self, *, global_token_uids: torch.Tensor, num_local_tokens: int,
                                sequence_parallel: bool, context_parallel_size: int) -> torch.Tensor:
-        uids = global_token_uids.to(dtype=torch.int64, device="cpu").reshape(-1)
-        if context_parallel_size > 1 and int(self._ps.get_context_parallel_world_size()) > 1:
-            raise RuntimeError("context-parallel token slicing needs megatron's "
-                               "get_batch_on_this_cp_rank, which this build does not provide")
+        uids = global_token_uids.detach().to(device="cpu", dtype=torch.int64).reshape(-1)
+        cp = int(self._ps.get_context_parallel_world_size())
+        if context_parallel_size > 1 and cp > 1:
+            chunks = uids.chunk(2 * cp)
+            r = int(self._ps.get_context_parallel_rank())
+            uids = torch.cat((chunks[r], chunks[2 * cp - 1 - r]))
         tp = int(self._ps.get_tensor_model_parallel_world_size())
         if sequence_parallel and tp > 1 and uids.numel() != num_local_tokens:
-            total = int(uids.numel())
-            if total % tp:
-                raise RuntimeError(
-                    "Routing replay cannot derive sequence-parallel local token uids from merged "
-                    f"rows: total_tokens={total}, tp_size={tp}, num_local_tokens={num_local_tokens}")
-            per = total // tp
-            if per != num_local_tokens:
-                raise RuntimeError(
-                    "Routing replay local token uid count mismatch after context-parallel "
-                    f"slicing: total_tokens={total}, tp_size={tp}, "
-                    f"expected_local_tokens={num_local_tokens}, tp_local_tokens={per}")
-            rank = int(self._ps.get_tensor_model_parallel_rank())
-            uids = uids[rank * per:(rank + 1) * per]
-        uids = uids.contiguous()
+            if uids.numel() % tp or uids.numel() // tp != num_local_tokens:
+                raise RuntimeError(f"{uids.numel()} token uids cannot be split over {tp} "
+                                   f"sequence-parallel ranks into {num_local_tokens} each")
+            r = int(self._ps.get_tensor_model_parallel_rank())
+            uids = uids[r * num_local_tokens:(r + 1) * num_local_tokens]
         if uids.numel() != num_local_tokens:
-            raise RuntimeError("Routing replay local token uid count mismatch: "
-                               f"expected={num_local_tokens}, got={uids.numel()}")
-        return uids
+            raise RuntimeError(f"expected {num_local_tokens} local token uids, got {uids.numel()}")
+        return uids.contiguous()
 
 
-# ---------------------------------------------------------------- controller
-@dataclass
-class _RouterCursor:
-    """Per-router progress through the step's call sequence."""
-    sequence: list[int]
-    pos: int = 0
-    last_index: int | None = None
-    last_key: tuple[str, int] | None = None
-    reuses: int = 0
+# ------------------------------------------------------------- controller parts
+MicroKey = tuple[str, int]
+
+
+class _CallCursor:
+    """Consumption of one router's calls in a step.
+
+    ``plan`` lists the call indices this rank runs, in order, and ``keys``
+    the micro each belongs to.  ``pending(active)`` is what the active micro
+    may run next; ``take(active)`` consumes it.  A call for the micro that
+    just consumed its route, when the plan has moved on to another micro, is
+    an activation recompute: it gets that route again."""
+
+    def __init__(self, plan: list[int], keys: list[MicroKey | None]) -> None:
+        self.plan, self.keys = plan, keys
+        self.pos = 0
+        self.last: tuple[int, MicroKey | None] | None = None
+        self.reuses = 0
+
+    def _recompute(self, active: MicroKey | None) -> bool:
+        return (active is not None and self.last is not None and self.last[1] == active
+                and (self.pos == len(self.plan) or self.keys[self.pos] != active))
+
+    def pending(self, active: MicroKey | None) -> list[int]:
+        if self._recompute(active):
+            return [self.last[0]]
+        if self.pos == len(self.plan):
+            return []
+        if active is None:
+            return [self.plan[self.pos]]
+        run = []
+        for ci, key in zip(self.plan[self.pos:], self.keys[self.pos:]):
+            if key != active:
+                break
+            run.append(ci)
+        return run
+
+    def take(self, active: MicroKey | None, allow_reuse: bool, where: str) -> int:
+        if self._recompute(active):
+            if not allow_reuse:
+                raise RuntimeError(f"{where}: recompute reuse is disabled, yet micro {active} "
+                                   "ran its router again")
+            self.reuses += 1
+            return self.last[0]
+        if self.pos == len(self.plan):
+            raise RuntimeError(f"{where}: more router calls than the {len(self.plan)} planned")
+        ci = self.plan[self.pos]
+        self.last = (ci, self.keys[self.pos])
+        self.pos += 1
+        return ci
+
+    @property
+    def done(self) -> bool:
+        return self.pos == len(self.plan)
+
+
+class _UidRows:
+    """Row of each token uid in the step's route tables.  Dense uid ranges
+    (the packed-sequence case) map by an offset; others through a sorted
+    index (searchsorted), vectorised either way.  Negative uids (tokens
+    without one) map to -1 - (their rank among the negative positions), the
+    side-table convention of the replay kernel."""
+
+    def __init__(self, uids: torch.Tensor) -> None:
+        self.n = int(uids.numel())
+        self.dense = None
+        if self.n and bool((uids[1:] - uids[:-1] == 1).all()):
+            self.dense = int(uids[0])
+        else:
+            self.sorted, self.order = torch.sort(uids)
+
+    def rows(self, uids: torch.Tensor, where: str) -> tuple[torch.Tensor, torch.Tensor]:
+        """(rows int64 [T], positions of the negative uids)."""
+        neg = torch.nonzero(uids < 0).flatten()
+        rows = torch.empty_like(uids)
+        valid = uids >= 0
+        v = uids[valid]
+        if self.dense is not None:
+            r = v - self.dense
+            bad = (r < 0) | (r >= self.n)
+            if bool(bad.any()):
+                raise RuntimeError(f"{where}: token uid {int(v[bad][0])} is outside the active "
+                                   f"dense step span [{self.dense}, {self.dense + self.n})")
+        else:
+            at = torch.searchsorted(self.sorted, v).clamp_max(max(self.n - 1, 0))
+            bad = (self.sorted[at] != v) if self.n else torch.ones_like(v, dtype=torch.bool)
+            if bool(bad.any()):
+                raise RuntimeError(f"{where}: token uid {int(v[bad][0])} is missing from the "
+                                   "step's global_token_uids")
+            r = self.order[at]
+        rows[valid] = r
+        rows[neg] = -1 - torch.arange(neg.numel())
+        return rows, neg
 
 
 @dataclass
 class _Binding:
+    key: str
     module: Any
     original_routing: Any
-    router_replay: Any
-    sequence_parallel: bool
-    context_parallel_size: int
+    replay: Any
     topk: int
+    sequence_parallel: bool
+
+
+@dataclass
+class _Micro:
+    """Targets staged for one micro: per uid layout, per router."""
+    uid_sets: dict[str, torch.Tensor] = field(default_factory=dict)
+    targets: dict[tuple[str, str], Any] = field(default_factory=dict)  # (layout, router) -> target
+    calls: dict[str, int] = field(default_factory=dict)               # router -> call staged
+    active: str | None = None
+    ready: Any = None          # event after the side-stream copies (device targets)
+    installed: dict[str, tuple[str, int]] = field(default_factory=dict)
 
 
 class MoeRoutingReplayController:
-    """Feeds each patched router the replay target of the current micro-batch
-    (routing_replay.py:696-1579).
+    """Drives megatron-style routers to replay a bundle's routes.
 
-    Life cycle per step: ``set_step`` -> for each micro ``begin_micro`` ->
-    ``set_local_input_token_uids`` / ``prepare_micro_targets`` (targets are
-    built on the host and staged to the device on a side stream, or, with
-    ``device_targets``, kept as the step's device route table plus the
-    micro's device row map) -> the
-    router's ``routing`` call installs the target -> ``finalize_step`` checks
-    every expected call was consumed.  A second routing call for the same
-    micro (activation recompute) reuses the previous call's route.
+    Per step: ``set_step`` (validate, plan each router's calls, upload the
+    step's route table) -> per micro ``begin_micro`` + ``set_local_input_token_uids``
+    / ``prepare_micro_targets`` (uids -> rows, targets staged) -> each router's
+    ``routing`` installs its target -> ``finalize_step`` checks that every
+    planned call ran.  ``device_targets`` (CUDA) hands the routers
+    ``DeviceReplayTarget`` views for the HIP replay kernel; otherwise targets
+    are [T, k] int64 tensors on ``device``.
     """
 
     def __init__(self, *, bundle: MoeRoutingReplayBundle, strict: bool,
                  local_token_indexer: Any | None = None, allow_recompute_reuse: bool = True,
-                 device: torch.device | str | None = None,
-                 parallel_state: Any | None = None, device_targets: bool = False) -> None:
+                 device: torch.device | str | None = None, parallel_state: Any | None = None,
+                 device_targets: bool = False) -> None:
         self.bundle = bundle
         self.strict = strict
         self.allow_recompute_reuse = allow_recompute_reuse
-        # device path: route tables uploaded once per step and row maps once
-        # per micro; routers replay table[rows[t]] (DeviceReplayTarget)
         self.device_targets = device_targets
         self.parallel_state = parallel_state or SingleProcessParallelState()
         self.local_token_indexer = local_token_indexer or TopologyAwareLocalTokenIndexer(
             self.parallel_state)
         self._device = torch.device(device) if device is not None else None
         self._bindings: dict[str, _Binding] = {}
-        self._target_buffers: dict[tuple[str, str, int], torch.Tensor] = {}
         self._copy_stream: torch.cuda.Stream | None = None
-        self._reset_step_state()
+        self._clear_step()
 
     # ------------------------------------------------------------ state
-    def _reset_step_state(self) -> None:
+    def _clear_step(self) -> None:
         self._step: int | None = None
-        self._step_routes: StepRoutes | None = None
-        self._sample: int | None = None
-        self._micro: int | None = None
-        self._cursors: dict[str, _RouterCursor] = {}
-        self._uid_dense_start: int | None = None
-        self._uid_count = 0
-        self._uid_rows: dict[int, int] = {}
-        if getattr(self, "_device_tables", None) and self._copy_stream is not None:
-            # the dropped tables' memory returns to the compute stream: order it after their copies
-            torch.cuda.current_stream(self._target_device()).wait_stream(self._copy_stream)
-        self._device_tables: dict[tuple[str, int], torch.Tensor] = {}
-        self._reset_staged()
+        self._routes: StepRoutes | None = None
+        self._cursors: dict[str, _CallCursor] = {}
+        self._uid_rows: _UidRows | None = None
+        self._tables: dict[tuple[str, int], torch.Tensor] = {}   # device views per call
+        self._micro_key: MicroKey | None = None
+        self._micro_order: int | None = None
+        self._micro = _Micro()
 
-    def _reset_staged(self) -> None:
-        self._uid_sets: dict[str, torch.Tensor] = {}
-        self._targets: dict[tuple[str, str, int], torch.Tensor] = {}
-        self._installed: dict[str, tuple[str, int]] = {}
-        self._host_staging: list[torch.Tensor] = []
-        self._device_rows: dict[tuple[str, bool], torch.Tensor] = {}
-        self._copy_event: torch.cuda.Event | None = None
-        self._copy_waited = True
-        self._active_uid_key: str | None = None
-
-    @property
-    def _local_router_keys(self) -> list[str]:
-        return sorted(self._bindings)
-
-    def update_bundle(self, *, bundle: MoeRoutingReplayBundle, strict: bool) -> None:
-        self.bundle = bundle
-        self.strict = strict
-        self.clear_replay_state()
-        if strict:
-            missing = [k for k in self._local_router_keys if k not in bundle.router_keys]
-            if missing:
-                raise RuntimeError(
-                    f"Router keys from model are missing in replay bundle: router_keys={missing}")
-
-    def clear_replay_state(self) -> None:
-        self._clear_replay_objects()
-        self._reset_step_state()
-
-    def _clear_replay_objects(self) -> None:
-        RouterReplay.clear_global_indices()
-        RouterReplay.clear_global_router_replay_action()
-        for b in self._bindings.values():
-            if not isinstance(b.router_replay, RouterReplay):
-                b.router_replay.set_router_replay_action(None)
-
-    def _target_device(self) -> torch.device:
+    def _device_for_targets(self) -> torch.device:
         if self._device is not None:
             return self._device
-        if torch.cuda.is_available():
-            return torch.device("cuda", torch.cuda.current_device())
-        return torch.device("cpu")
+        return torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() \
+            else torch.device("cpu")
 
-    # --------------------------------------------------------- patching
+    def _on_gpu(self) -> bool:
+        return self.device_targets and self._device_for_targets().type == "cuda"
+
+    def call_plan(self, router_key: str) -> list[int]:
+        """Call indices router ``router_key`` consumes this step, in order."""
+        return list(self._cursors[router_key].plan)
+
+    def update_bundle(self, *, bundle: MoeRoutingReplayBundle, strict: bool) -> None:
+        self.bundle, self.strict = bundle, strict
+        self.clear_replay_state()
+        if strict:
+            absent = sorted(k for k in self._bindings if k not in bundle.router_keys)
+            if absent:
+                raise RuntimeError(f"Router keys from model are missing in replay bundle: {absent}")
+
+    def clear_replay_state(self) -> None:
+        RouterReplay.clear_global_indices()
+        RouterReplay.clear_global_router_replay_action()
+        self._clear_step()
+
+    # ------------------------------------------------------------ patching
     def install_router_patches(self, model_chunks: list[Any]) -> None:
-        """Wrap ``routing`` of every ``*.mlp.router`` module so that the replay
-        target of the active micro is installed right before it runs."""
-        global _active_controller
+        """Wrap ``routing`` of every ``*.mlp.router`` module so that its replay
+        target is installed right before it runs."""
+        global _installed
         if self._bindings:
             return
         for chunk_index, chunk in enumerate(model_chunks):
             for name, module in chunk.named_modules():
                 if ROUTER_NAME_TOKEN not in name or not hasattr(module, "routing"):
                     continue
-                rk = build_router_key_from_module_name(chunk_index=chunk_index, module_name=name)
-                if self.strict and rk not in self.bundle.router_keys:
-                    raise RuntimeError(
-                        f"Router key from model is missing in replay bundle: router_key='{rk}'")
-                config = getattr(module, "config", None)
-                if bool(getattr(config, "moe_router_fusion", False)):
-                    raise RuntimeError(
-                        "MoE routing replay requires moe_router_fusion=False because Megatron "
-                        f"Core fused routing bypasses RouterReplay: router_key='{rk}'")
+                key = build_router_key_from_module_name(chunk_index=chunk_index, module_name=name)
+                cfg = getattr(module, "config", None)
                 replay = getattr(module, "router_replay", None)
-                if replay is None:
-                    raise RuntimeError(
-                        "MoE routing replay requires provider.moe_enable_routing_replay=True "
-                        f"before model construction: router_key='{rk}'")
-                if getattr(replay, "_art_routing_replay_patched", False):
-                    raise RuntimeError(f"RouterReplay instance is already patched: router_key='{rk}'")
-                if getattr(module, "_art_routing_replay_target_patched", False):
-                    raise RuntimeError(
-                        f"Router module routing method is already patched: router_key='{rk}'")
+                problem = None
+                if self.strict and key not in self.bundle.router_keys:
+                    problem = "its key is not in the replay bundle"
+                elif getattr(cfg, "moe_router_fusion", False):
+                    problem = ("replay needs moe_router_fusion=False (the fused router bypasses "
+                               "RouterReplay)")
+                elif replay is None:
+                    problem = ("replay needs the model built with "
+                               "provider.moe_enable_routing_replay=True (no router_replay)")
+                elif getattr(module, "_art_routing_replay_target_patched", False):
+                    problem = "its routing is already patched"
+                if problem:
+                    raise RuntimeError(f"router '{key}': {problem}")
                 original = module.routing
-                install = torch.compiler.disable(
-                    lambda _rk=rk: self._prepare_native_target_for_router(_rk))
+                hook = torch.compiler.disable(lambda _k=key: self._install_target(_k))
 
-                def routing_with_replay_target(_module, *args, _orig=original, _install=install,
-                                               **kwargs):
-                    _install()
+                def routing(mod, *args, _orig=original, _hook=hook, **kwargs):
+                    _hook()
                     return _orig(*args, **kwargs)
 
-                module.routing = types.MethodType(routing_with_replay_target, module)
+                module.routing = types.MethodType(routing, module)
                 module._art_routing_replay_target_patched = True
-                self._bindings[rk] = _Binding(
-                    module=module, original_routing=original, router_replay=replay,
-                    sequence_parallel=bool(getattr(config, "sequence_parallel", False)),
-                    context_parallel_size=int(getattr(config, "context_parallel_size", 1)),
-                    topk=int(module.topk))
-        _active_controller = self
+                self._bindings[key] = _Binding(key, module, original, replay, int(module.topk),
+                                               bool(getattr(cfg, "sequence_parallel", False)))
+        _installed = weakref.ref(self)
 
     def remove_router_patches(self) -> None:
-        global _active_controller
-        if _active_controller is self:
-            _active_controller = None
+        global _installed
+        if active_routing_replay_controller() is self:
+            _installed = None
         for b in self._bindings.values():
             b.module.routing = b.original_routing
             if hasattr(b.module, "_art_routing_replay_target_patched"):
-                delattr(b.module, "_art_routing_replay_target_patched")
-        self._clear_replay_objects()
+                del b.module._art_routing_replay_target_patched
         self._bindings.clear()
-        self._target_buffers.clear()
-        self._reset_step_state()
+        self.clear_replay_state()
 
     # ------------------------------------------------------------ steps
+    def _micro_key_of(self, sample: int | None, local_micro: int) -> MicroKey:
+        if sample is not None:
+            return ("sample", int(sample))
+        ps = self.parallel_state
+        return ("dummy_micro_slot",
+                local_micro * int(ps.get_data_parallel_world_size()) + int(ps.get_data_parallel_rank()))
+
+    def _plan(self, rk: str, sample_index, per_step: int | None) -> list[int]:
+        calls = self._routes.routers[rk].calls
+        where = f"step {self._step} router '{rk}'"
+        if all(r.call_key is not None for r in calls.values()):
+            by_micro: dict[MicroKey, list[int]] = {}
+            for ci in sorted(calls):
+                by_micro.setdefault(calls[ci].call_key, []).append(ci)
+            samples = sample_index if isinstance(sample_index, list) else [sample_index]
+            plan: list[int] = []
+            for local, sample in enumerate(samples):
+                key = self._micro_key_of(sample, local)
+                if key not in by_micro:
+                    raise RuntimeError(f"{where}: no calls for micro {key}")
+                plan += by_micro[key]
+            return plan
+        # legacy layout (no per-call micro metadata): contiguous blocks per sample
+        n = len(calls)
+        if sample_index is None:
+            if n != 1:
+                raise RuntimeError(f"{where}: the bundle lacks sample metadata and has {n} calls")
+            return [0]
+        samples = [s for s in (sample_index if isinstance(sample_index, list) else [sample_index])
+                   if s is not None]
+        count = per_step if per_step is not None else (
+            len(samples) if isinstance(sample_index, list) else 1)
+        if count <= 0 or n % count:
+            raise RuntimeError(f"{where}: {n} router calls are not divisible by the step's "
+                               f"{count} samples")
+        each = n // count
+        plan = []
+        for s in samples:
+            off = int(s) - self._step * count
+            if not 0 <= off < count:
+                raise RuntimeError(f"{where}: sample {s} is outside the step's samples "
+                                   f"[{self._step * count}, {self._step * count + count})")
+            plan += range(off * each, off * each + each)
+        return plan
+
     def set_step(self, *, step_index: int, sample_index: int | list[int | None] | None,
                  global_grad_accumulation_sequences: int | None = None) -> None:
+        """Start step ``step_index`` for this rank's samples (one per local micro;
+        None for a padded micro slot)."""
         if step_index not in self.bundle.steps:
-            raise RuntimeError(f"Replay bundle missing step_index={step_index}. "
-                               f"Available steps={sorted(self.bundle.steps)}")
-        sr = self.bundle.steps[step_index]
-        self._reset_step_state()
-        self._step, self._step_routes = step_index, sr
-        if isinstance(sample_index, list):
-            self._sample = next((s for s in sample_index if s is not None), None)
-        else:
-            self._sample = sample_index
-        uids = sr.global_token_uids
-        self._uid_count = int(uids.numel())
-        self._uid_dense_start = self._dense_start(uids)
-        if self._uid_dense_start is None:
-            self._uid_rows = {int(u): row for row, u in enumerate(uids.tolist())}
-        for rk in self._local_router_keys:
-            if rk not in sr.routers:
-                raise RuntimeError("Replay bundle step is missing local router key: "
-                                   f"step={step_index}, router='{rk}'")
+            raise RuntimeError(f"Replay bundle missing step_index={step_index}; it has steps "
+                               f"{sorted(self.bundle.steps)}")
+        self._clear_step()
+        self._step, self._routes = step_index, self.bundle.steps[step_index]
+        for rk in sorted(self._bindings):
+            if rk not in self._routes.routers:
+                raise RuntimeError(f"step {step_index} has no routes for router '{rk}'")
             topk = self._bindings[rk].topk
-            for ci, route in sr.routers[rk].calls.items():
+            for ci, route in self._routes.routers[rk].calls.items():
                 if not bool(route.expert_mask.all()):
-                    raise RuntimeError("masked slots are unsupported by Megatron native MoE routing "
-                                       f"replay: step={step_index}, router='{rk}', call={ci}")
+                    raise RuntimeError(f"masked slots are unsupported by native MoE routing replay "
+                                       f"(step {step_index}, router '{rk}', call {ci})")
                 if route.max_topk != topk:
-                    raise RuntimeError(
-                        "Replay route topk does not match Megatron router topk: "
-                        f"step={step_index}, router='{rk}', call={ci}, "
-                        f"route_topk={route.max_topk}, router_topk={topk}")
-            self._cursors[rk] = _RouterCursor(self._call_sequence(
-                rk, sample_index, global_grad_accumulation_sequences))
+                    raise RuntimeError(f"replayed route topk does not match the router: step "
+                                       f"{step_index}, router '{rk}', call {ci} has "
+                                       f"{route.max_topk}, the router {topk}")
+            plan = self._plan(rk, sample_index, global_grad_accumulation_sequences)
+            calls = self._routes.routers[rk].calls
+            self._cursors[rk] = _CallCursor(plan, [calls[ci].call_key for ci in plan])
+        self._uid_rows = _UidRows(self._routes.global_token_uids)
+        if self._on_gpu() and self._bindings:
+            self._upload_step_table()
         RouterReplay.clear_global_indices()
         RouterReplay.set_global_router_replay_action(RouterReplayAction.REPLAY_FORWARD)
 
     def finalize_step(self) -> None:
-        if self._step_routes is None:
+        """Check that every router consumed exactly its planned calls."""
+        if self._routes is None:
             raise RuntimeError("finalize_step called before set_step")
-        for rk in self._local_router_keys:
-            cur = self._cursors.get(rk)
-            if cur is None:
-                raise RuntimeError("Routing replay call sequence missing for router key: "
-                                   f"step={self._step}, router='{rk}'")
-            if cur.pos != len(cur.sequence):
-                raise RuntimeError("Routing replay step consumption mismatch: "
-                                   f"step={self._step}, router='{rk}', consumed={cur.pos}, "
-                                   f"expected={len(cur.sequence)}")
-        reuses = {rk: c.reuses for rk, c in sorted(self._cursors.items()) if c.reuses}
-        if reuses:
-            logger.info("Routing replay reused routes for recompute: step=%s counts=%s",
-                        self._step, reuses)
-        self._clear_replay_objects()
-        self._reset_step_state()
-
-    @staticmethod
-    def _dense_start(uids: torch.Tensor) -> int | None:
-        """First uid when the uids are consecutive (row = uid - start), else None."""
-        n = int(uids.numel())
-        if n == 0:
-            return None
-        if n == 1 or bool((uids[1:] - uids[:-1] == 1).all()):
-            return int(uids[0])
-        return None
-
-    # ------------------------------------------------- call bookkeeping
-    def _dummy_key(self, local_micro_index: int) -> tuple[str, int]:
-        ps = self.parallel_state
-        return ("dummy_micro_slot", local_micro_index * int(ps.get_data_parallel_world_size())
-                + int(ps.get_data_parallel_rank()))
-
-    def _micro_key(self, sample: int | None, local_micro_index: int) -> tuple[str, int]:
-        return ("sample", int(sample)) if sample is not None else self._dummy_key(local_micro_index)
-
-    def _active_key(self) -> tuple[str, int] | None:
-        return None if self._micro is None else self._micro_key(self._sample, self._micro)
-
-    def _call_sequence(self, rk: str, sample_index, gga: int | None) -> list[int]:
-        """Order in which this rank consumes the step's calls of router ``rk``."""
-        calls = self._step_routes.routers[rk].calls
-        if all(r.call_key is not None for r in calls.values()):
-            by_key: dict[tuple[str, int], list[int]] = defaultdict(list)
-            for ci in sorted(calls):
-                by_key[calls[ci].call_key].append(ci)
-            if isinstance(sample_index, list):
-                local_keys = [self._micro_key(s, i) for i, s in enumerate(sample_index)]
-            else:
-                local_keys = [self._micro_key(sample_index, 0)]
-            seq: list[int] = []
-            for key in local_keys:
-                if not by_key.get(key):
-                    raise RuntimeError("Replay router call sequence is missing local micro metadata: "
-                                       f"step={self._step}, router='{rk}', call_key={key}")
-                seq.extend(by_key[key])
-            return seq
-        # calls without micro metadata: contiguous blocks of calls per sample
-        total = len(calls)
-        if sample_index is None:
-            if total != 1:
-                raise RuntimeError(f"Replay router call sequence lacks sample metadata and has "
-                                   f"{total} calls for router='{rk}', step={self._step}")
-            return [0]
-        samples = [s for s in sample_index if s is not None] if isinstance(sample_index, list) \
-            else [sample_index]
-        per_step = gga if gga is not None else len(samples)
-        if per_step <= 0 or total % per_step:
-            raise RuntimeError("Replay router call count is not divisible by step sample count: "
-                               f"step={self._step}, router='{rk}', total_calls={total}, "
-                               f"step_sample_count={per_step}")
-        per_sample = total // per_step
-        base = self._step * per_step
-        seq = []
-        for s in samples:
-            off = int(s) - base
-            if not 0 <= off < per_step:
-                raise RuntimeError("Replay router call index is outside the step-local range: "
-                                   f"step={self._step}, router='{rk}', sample_index={s}, "
-                                   f"step_base_sample_index={base}, step_sample_count={per_step}")
-            seq.extend(range(off * per_sample, (off + 1) * per_sample))
-        return seq
-
-    def _active_calls(self, rk: str) -> list[int]:
-        """Calls of router ``rk`` that belong to the active micro (the previous
-        call again when the micro re-runs its forward)."""
-        if self._step_routes is None:
-            raise RuntimeError("Routing replay begin_micro called before set_step")
-        calls = self._step_routes.routers[rk].calls
-        cur = self._cursors[rk]
-        key = self._active_key()
-        repeat = key is not None and cur.last_index is not None and cur.last_key == key
-        if cur.pos >= len(cur.sequence):
-            return [cur.last_index] if repeat else []
-        if key is None:
-            return [cur.sequence[cur.pos]]
-        if repeat and calls[cur.sequence[cur.pos]].call_key != key:
-            return [cur.last_index]
-        run = []
-        for ci in cur.sequence[cur.pos:]:
-            if calls[ci].call_key != key:
-                break
-            run.append(ci)
-        return run
-
-    def _next_call(self, rk: str) -> int:
-        """Consume (or, for a recompute, reuse) the next call of router ``rk``."""
-        if self._step_routes is None:
-            raise RuntimeError("Routing replay router call occurred before set_step")
-        cur = self._cursors.get(rk)
-        if cur is None:
-            raise RuntimeError("Routing replay call sequence missing for router key: "
-                               f"step={self._step}, router='{rk}'")
-        calls = self._step_routes.routers[rk].calls
-        key = self._active_key()
-        nxt = calls[cur.sequence[cur.pos]].call_key if cur.pos < len(cur.sequence) else None
-        if key is not None and cur.last_index is not None and cur.last_key == key and nxt != key:
-            if not self.allow_recompute_reuse:
-                raise RuntimeError("Routing replay recompute reuse is disabled: "
-                                   f"step={self._step}, router='{rk}', call_key={key}")
-            cur.reuses += 1
-            return cur.last_index
-        if cur.pos >= len(cur.sequence):
-            raise RuntimeError("Routing replay call cursor exceeded local call sequence: "
-                               f"step={self._step}, router='{rk}', cursor={cur.pos}, "
-                               f"sequence_length={len(cur.sequence)}")
-        ci = cur.sequence[cur.pos]
-        cur.pos += 1
-        cur.last_index, cur.last_key = ci, calls[ci].call_key
-        return ci
+        for rk, cur in sorted(self._cursors.items()):
+            if not cur.done:
+                raise RuntimeError(f"Routing replay step consumption mismatch: step {self._step}, "
+                                   f"router '{rk}' ran {cur.pos} of {len(cur.plan)} planned calls")
+        reused = {rk: c.reuses for rk, c in self._cursors.items() if c.reuses}
+        if reused:
+            logger.info("routing replay step %s: routes reused for recompute %s", self._step, reused)
+        self.clear_replay_state()
 
     # ------------------------------------------------------------ micros
     def begin_micro(self, sample_index: int | None, micro_order: int) -> None:
-        self._sample, self._micro = sample_index, micro_order
-        for rk in self._local_router_keys:
-            calls = self._active_calls(rk)
-            if len(calls) != 1:
-                raise RuntimeError("Routing replay expected exactly one router call per local "
-                                   f"microbatch for router='{rk}', got {calls}")
+        """Make micro ``micro_order`` (of ``sample_index``) the active one; each
+        router must have exactly one call for it."""
+        self._micro_key = self._micro_key_of(sample_index, micro_order)
+        self._micro_order = micro_order
+        for rk in sorted(self._cursors):
+            pending = self._cursors[rk].pending(self._micro_key)
+            if len(pending) != 1:
+                raise RuntimeError(f"Routing replay expected exactly one router call per micro for "
+                                   f"router '{rk}', got calls {pending}")
 
     def set_local_input_token_uids(self, local_token_uids: torch.Tensor | None) -> None:
         self.prepare_micro_targets({"attention": local_token_uids})
 
     def prepare_micro_targets(self, token_uid_sets: Mapping[str, torch.Tensor | None], *,
                               active_token_uid_key: str = "attention") -> None:
-        """Build and stage the targets of every router for each token layout."""
-        if self._step_routes is None or self._micro is None:
-            raise RuntimeError("Routing replay target staging requires set_step and begin_micro")
-        self._reset_staged()
-        sets = {k: self._normalize_uids(v) for k, v in token_uid_sets.items() if v is not None}
-        if not sets:
-            raise RuntimeError("Routing replay requires at least one token UID set")
+        """Stage the active micro's targets for each token layout (e.g. the
+        attention order and a linear-attention order of the same tokens)."""
+        if self._routes is None or self._micro_order is None:
+            raise RuntimeError("target staging needs set_step and begin_micro first")
+        sets = {}
+        for name, uids in token_uid_sets.items():
+            if uids is None:
+                continue
+            if uids.device.type != "cpu":
+                raise RuntimeError("token uids must be CPU metadata (a device tensor would force "
+                                   "a host sync in the model path)")
+            sets[name] = uids.detach().to(torch.int64).reshape(-1).contiguous()
         if active_token_uid_key not in sets:
-            raise RuntimeError("Routing replay active token UID key was not prepared: "
-                               f"key='{active_token_uid_key}', prepared={sorted(sets)}")
-        self._uid_sets = sets
-        if not self._bindings:
-            self._active_uid_key = active_token_uid_key
-            return
-        use_device = self.device_targets and self._target_device().type == "cuda"
-        for uk, uids in sets.items():
-            for rk in self._local_router_keys:
-                calls = self._active_calls(rk)
-                if len(calls) != 1:
-                    raise RuntimeError("Routing replay expected exactly one active router call while "
-                                       f"staging targets for router='{rk}', got {calls}")
-                b = self._bindings[rk]
-                router_uids = self._token_uids_for_router_binding(
-                    uids, sequence_parallel=b.sequence_parallel)
-                if use_device and bool((router_uids >= 0).all()):
-                    # padded uids (< 0) take synthetic rows: those micros stay on the host path
-                    self._stage_device((uk, rk, calls[0]), router_uids, b.sequence_parallel)
-                    continue
-                target = self._explicit_target_for_router_call(
-                    router_key=rk, call_index=calls[0], explicit_uids=router_uids)
-                self._stage((uk, rk, calls[0]), target)
-        if self._copy_stream is not None and not self._copy_waited:
-            self._copy_event = torch.cuda.Event()
-            self._copy_event.record(self._copy_stream)
+            raise RuntimeError(f"token uid layout '{active_token_uid_key}' was not given "
+                               f"(got {sorted(sets)})")
+        self._micro = _Micro(uid_sets=sets)
+        for rk in sorted(self._bindings):
+            pending = self._cursors[rk].pending(self._micro_key)
+            if len(pending) != 1:
+                raise RuntimeError(f"Routing replay expected exactly one router call per micro for "
+                                   f"router '{rk}', got calls {pending}")
+            self._micro.calls[rk] = pending[0]
+        if self._on_gpu():
+            self._stage_on_device()
+        else:
+            self._stage_on_host()
         self.set_active_token_uid_key(active_token_uid_key)
 
     def set_active_token_uid_key(self, token_uid_key: str) -> None:
-        if self._bindings and token_uid_key not in {k[0] for k in self._targets}:
-            raise RuntimeError("Routing replay token UID key was not staged for this micro: "
-                               f"key='{token_uid_key}', staged={sorted({k[0] for k in self._targets})}")
-        self._active_uid_key = token_uid_key
-
-    @staticmethod
-    def _normalize_uids(uids: torch.Tensor) -> torch.Tensor:
-        if uids.device.type != "cpu":
-            raise RuntimeError(
-                "Routing replay token UIDs must be CPU metadata. Passing CUDA token UIDs would "
-                "force a host/device synchronization in the model path.")
-        return uids.detach().to(torch.int64).contiguous().reshape(-1)
+        if self._bindings and token_uid_key not in self._micro.uid_sets:
+            raise RuntimeError(f"token uid layout '{token_uid_key}' was not staged for this micro "
+                               f"(staged: {sorted(self._micro.uid_sets)})")
+        self._micro.active = token_uid_key
 
     def local_token_uids_for_active_dispatch(self, *, num_local_tokens: int,
                                              sequence_parallel: bool) -> torch.Tensor | None:
-        if self._active_uid_key is None:
-            return None
-        uids = self._uid_sets.get(self._active_uid_key)
+        """The active layout's uids as this rank dispatches them (padding
+        dropped when that is what makes the count match), or None."""
+        uids = self._micro.uid_sets.get(self._micro.active) if self._micro.active else None
         if uids is None:
             return None
-        local = self._token_uids_for_router_binding(uids, sequence_parallel=sequence_parallel)
+        local = self._sp_slice(uids, sequence_parallel)
         if local.numel() == num_local_tokens:
-            return local.contiguous()
-        compact = local[local >= 0]
-        return compact.contiguous() if compact.numel() == num_local_tokens else None
+            return local
+        real = local[local >= 0]
+        return real.contiguous() if real.numel() == num_local_tokens else None
 
-    def _token_uids_for_router_binding(self, token_uids: torch.Tensor, *,
-                                       sequence_parallel: bool) -> torch.Tensor:
-        """This tensor-parallel rank's ceil(N/tp) slice under sequence
-        parallelism, padded with uid -1 (routing_replay.py:1506-1528)."""
-        if not sequence_parallel:
-            return token_uids
+    def _sp_slice(self, uids: torch.Tensor, sequence_parallel: bool) -> torch.Tensor:
+        """A sequence-parallel router sees its tensor-parallel rank's
+        ceil(T / tp) tokens, the last rank's share padded with -1."""
         tp = int(self.parallel_state.get_tensor_model_parallel_world_size())
-        if tp <= 1:
-            return token_uids
-        rank = int(self.parallel_state.get_tensor_model_parallel_rank())
-        n = int(token_uids.numel())
-        per = (n + tp - 1) // tp
-        lo, hi = rank * per, min(rank * per + per, n)
-        out = token_uids.new_full((per,), -1)
-        if lo < n:
-            out[:hi - lo] = token_uids[lo:hi]
+        if not sequence_parallel or tp <= 1:
+            return uids
+        share = -(-uids.numel() // tp)
+        part = uids[int(self.parallel_state.get_tensor_model_parallel_rank()) * share:][:share]
+        out = uids.new_full((share,), -1)
+        out[:part.numel()] = part
         return out
 
-    def _explicit_target_for_router_call(self, *, router_key: str, call_index: int,
-                                         explicit_uids: torch.Tensor) -> torch.Tensor:
-        """[N, k] int64 target: the bundle row of each uid, synthetic rows for
-        uid < 0 (routing_replay.py:1437-1474)."""
-        if self._step_routes is None:
-            raise RuntimeError("Routing replay explicit target used before set_step")
-        route = self._step_routes.routers[router_key].calls[call_index]
-        uids = explicit_uids.reshape(-1).contiguous()
-        target = torch.empty((uids.numel(), route.max_topk), dtype=torch.long)
-        ok = torch.nonzero(uids >= 0).reshape(-1)
-        if ok.numel():
-            rows = self._rows_for_uids(uids[ok], router_key, call_index)
-            target[ok] = route.expert_indices.index_select(0, rows).long()
-        pad = torch.nonzero(uids < 0).reshape(-1)
-        if pad.numel():
-            target[pad] = synthetic_replay_rows(
-                row_positions=pad, num_experts=route.num_experts, topk=route.max_topk,
-                dtype=torch.long,
-                seed=(int(self._step or 0) + 1) * _SEED_SAMPLE + (call_index + 1) * _SEED_LAYER)
-        return target.contiguous()
+    def _synthetic(self, call: int, positions: torch.Tensor, e: int, k: int) -> torch.Tensor:
+        return synthetic_replay_rows(
+            row_positions=positions, num_experts=e, topk=k, dtype=torch.int32,
+            seed=(int(self._step or 0) + 1) * _SEED_SAMPLE + (call + 1) * _SEED_LAYER)
 
-    def _rows_for_uids(self, uids: torch.Tensor, rk: str, ci: int) -> torch.Tensor:
-        if self._uid_dense_start is not None:
-            rows = uids.long() - self._uid_dense_start
-            bad = (rows < 0) | (rows >= self._uid_count)
-            if bool(bad.any()):
-                raise RuntimeError("Explicit routing replay token uid is outside the active dense "
-                                   f"step span: step={self._step}, router='{rk}', call={ci}, "
-                                   f"uid={int(uids[bad][0])}")
-            return rows
-        try:
-            return torch.tensor([self._uid_rows[u] for u in uids.tolist()], dtype=torch.long)
-        except KeyError as exc:
-            raise RuntimeError("Explicit routing replay token uid is missing from the active step "
-                               f"map: step={self._step}, router='{rk}', call={ci}, "
-                               f"uid={exc.args[0]}") from exc
+    def _stage_on_host(self) -> None:
+        dev = self._device_for_targets()
+        for name, uids in self._micro.uid_sets.items():
+            for rk, b in self._bindings.items():
+                ci = self._micro.calls[rk]
+                route = self._routes.routers[rk].calls[ci]
+                where = f"step {self._step} router '{rk}' call {ci}"
+                local = self._sp_slice(uids, b.sequence_parallel)
+                rows, neg = self._uid_rows.rows(local, where)
+                if bool((rows >= route.num_global_tokens).any()):
+                    raise RuntimeError(f"{where}: a token row is past the route's "
+                                       f"{route.num_global_tokens} rows")
+                target = route.expert_indices.index_select(0, rows.clamp_min(0)).long()
+                if neg.numel():
+                    target[neg] = self._synthetic(ci, neg, route.num_experts, route.max_topk).long()
+                self._micro.targets[(name, rk)] = self._upload(target) if dev.type == "cuda" \
+                    else target
+        if dev.type == "cuda" and self._micro.targets:
+            ready = torch.cuda.Event()
+            ready.record(self._side_stream())
+            self._micro.ready = ready
 
-    def _stage(self, key: tuple[str, str, int], target_cpu: torch.Tensor) -> None:
-        """Keep the target on the host (CPU device) or start its copy into a
-        reused device buffer on a side stream from pinned host memory."""
-        target_cpu = target_cpu.long().contiguous()
-        dev = self._target_device()
-        if dev.type != "cuda":
-            self._targets[key] = target_cpu
-            return
+    # ------------------------------------------------------------ device side
+    def _side_stream(self) -> torch.cuda.Stream:
         if self._copy_stream is None:
-            self._copy_stream = torch.cuda.Stream(device=dev)
-        host = target_cpu if target_cpu.is_pinned() else target_cpu.pin_memory()
-        self._host_staging.append(host)
-        buf = self._target_buffers.get(key)
-        if buf is None or buf.shape != host.shape or buf.device != dev:
-            buf = torch.empty(host.shape, dtype=torch.long, device=dev)
-            self._target_buffers[key] = buf
-        # the copy must not overwrite a buffer the compute stream may still read
-        self._copy_stream.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(self._copy_stream):
-            buf.copy_(host, non_blocking=True)
-        self._targets[key] = buf
-        self._copy_waited = False
+            self._copy_stream = torch.cuda.Stream(device=self._device_for_targets())
+        return self._copy_stream
 
-    def _copy_to_device(self, host: torch.Tensor) -> torch.Tensor:
-        """Start an async copy of ``host`` (pinned) into a new device buffer on
-        the side stream; the buffer belongs to the compute stream."""
-        dev = self._target_device()
-        if self._copy_stream is None:
-            self._copy_stream = torch.cuda.Stream(device=dev)
-        host = host.contiguous()
-        host = host if host.is_pinned() else host.pin_memory()
-        self._host_staging.append(host)
+    def _upload(self, host: torch.Tensor) -> torch.Tensor:
+        """Device copy of ``host`` made on the side stream (after the compute
+        stream's queued work, which may still read the buffer's last owner)."""
+        dev = self._device_for_targets()
+        side = self._side_stream()
         buf = torch.empty(host.shape, dtype=host.dtype, device=dev)
-        self._copy_stream.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(self._copy_stream):
-            buf.copy_(host, non_blocking=True)
-        self._copy_waited = False
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            buf.copy_(host.pin_memory(), non_blocking=True)
+        buf.record_stream(side)
         return buf
 
-    def _stage_device(self, key: tuple[str, str, int], uids: torch.Tensor,
-                      sequence_parallel: bool) -> None:
-        """Device path: the step's route table of the call (uploaded once per
-        step) and the micro's row map (uploaded once per token layout)."""
-        uk, rk, ci = key
-        table = self._device_tables.get((rk, ci))
-        if table is None:
-            route = self._step_routes.routers[rk].calls[ci]
-            table = self._copy_to_device(route.expert_indices.to(torch.int32))
-            self._device_tables[(rk, ci)] = table
-        rows = self._device_rows.get((uk, sequence_parallel))
-        if rows is None:
-            rows = self._copy_to_device(self._rows_for_uids(uids, rk, ci).to(torch.int32))
-            self._device_rows[(uk, sequence_parallel)] = rows
-        self._targets[key] = DeviceReplayTarget(table, rows)
+    def _upload_step_table(self) -> None:
+        """Every call this rank will consume, all routers, in one device table
+        per topk: one host-to-device copy per step."""
+        by_k: dict[int, list[tuple[str, int, RouterCallRoute]]] = {}
+        for rk, cur in sorted(self._cursors.items()):
+            for ci in dict.fromkeys(cur.plan):
+                route = self._routes.routers[rk].calls[ci]
+                by_k.setdefault(route.max_topk, []).append((rk, ci, route))
+        for k, entries in by_k.items():
+            table = self._upload(torch.cat([r.expert_indices for _, _, r in entries]))
+            base = 0
+            for rk, ci, route in entries:
+                n = route.num_global_tokens
+                self._tables[(rk, ci)] = table[base:base + n]
+                base += n
+
+    def _stage_on_device(self) -> None:
+        """Row maps once per (layout, sequence-parallel slicing), shared by all
+        routers; synthetic side tables per call when some tokens lack a uid."""
+        maps: dict[tuple[str, bool], tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = {}
+        for name, uids in self._micro.uid_sets.items():
+            for rk, b in self._bindings.items():
+                ci = self._micro.calls[rk]
+                route = self._routes.routers[rk].calls[ci]
+                where = f"step {self._step} router '{rk}' call {ci}"
+                mk = (name, b.sequence_parallel)
+                if mk not in maps:
+                    rows, neg = self._uid_rows.rows(self._sp_slice(uids, b.sequence_parallel), where)
+                    maps[mk] = (self._upload(rows.to(torch.int32)), neg,
+                                rows.max() if rows.numel() else torch.tensor(-1))
+                rows_dev, neg, top = maps[mk]
+                if int(top) >= route.num_global_tokens:
+                    raise RuntimeError(f"{where}: a token row is past the route's "
+                                       f"{route.num_global_tokens} rows")
+                extra = None
+                if neg.numel():
+                    extra = self._upload(self._synthetic(ci, neg, route.num_experts,
+                                                         route.max_topk))
+                self._micro.targets[(name, rk)] = DeviceReplayTarget(self._tables[(rk, ci)],
+                                                                      rows_dev, extra)
+        ready = torch.cuda.Event()
+        ready.record(self._side_stream())
+        self._micro.ready = ready
 
     def wait_for_staged_targets(self) -> None:
-        if self._copy_event is None or self._copy_waited:
-            return
-        torch.cuda.current_stream(self._target_device()).wait_event(self._copy_event)
-        self._copy_waited = True
+        """Order the compute stream after the staged targets' copies."""
+        if self._micro.ready is not None:
+            torch.cuda.current_stream(self._device_for_targets()).wait_event(self._micro.ready)
+            self._micro.ready = None
 
-    def _prepare_native_target_for_router(self, router_key: str) -> None:
-        """Install the active micro's target on router ``router_key`` (runs
-        right before its ``routing``; routing_replay.py:1388-1435)."""
-        if self._step_routes is None or self._micro is None or self._active_uid_key is None:
-            raise RuntimeError("Routing replay router call occurred before staged targets were "
-                               f"ready: router='{router_key}'")
-        calls = self._active_calls(router_key)
-        if len(calls) != 1:
-            raise RuntimeError("Routing replay expected exactly one active router call while "
-                               f"preparing native replay for router='{router_key}', got {calls}")
-        ci = self._next_call(router_key)
-        if ci != calls[0]:
-            raise RuntimeError("Routing replay cursor mismatch while preparing native replay: "
-                               f"router='{router_key}', expected={calls[0]}, actual={ci}")
-        tkey = (self._active_uid_key, ci)
-        if self._installed.get(router_key) == tkey:
-            return
+    # ------------------------------------------------------------ at routing time
+    def _install_target(self, router_key: str) -> None:
+        """Runs right before router ``router_key`` routes: consume its call and
+        give its RouterReplay the staged target."""
+        m = self._micro
+        if self._routes is None or self._micro_order is None or m.active is None:
+            raise RuntimeError(f"router '{router_key}' ran before its replay targets were staged")
+        cur = self._cursors[router_key]
+        pending = cur.pending(self._micro_key)
+        if len(pending) != 1:
+            raise RuntimeError(f"Routing replay expected exactly one router call per micro for "
+                               f"router '{router_key}', got calls {pending}")
+        ci = cur.take(self._micro_key, self.allow_recompute_reuse,
+                      f"step {self._step} router '{router_key}'")
+        if ci != m.calls.get(router_key):
+            raise RuntimeError(f"router '{router_key}' consumed call {ci}, staged "
+                               f"{m.calls.get(router_key)}")
+        if m.installed.get(router_key) == (m.active, ci):
+            return                                   # recompute: target already in place
         self.wait_for_staged_targets()
-        target = self._targets.get((self._active_uid_key, router_key, ci))
-        if target is None:
-            raise RuntimeError("Routing replay target was not staged before router execution: "
-                               f"step={self._step}, router='{router_key}', call={ci}, "
-                               f"token_uid_key='{self._active_uid_key}'")
+        target = m.targets[(m.active, router_key)]
         b = self._bindings[router_key]
         if int(target.shape[1]) != b.topk:
-            raise RuntimeError("Routing replay target topk mismatch at router call: "
-                               f"router='{router_key}', call={ci}, "
-                               f"target_topk={int(target.shape[1])}, router_topk={b.topk}")
-        b.router_replay.set_target_indices(target)
-        b.router_replay.set_router_replay_action(RouterReplayAction.REPLAY_FORWARD)
-        self._installed[router_key] = tkey
+            raise RuntimeError(f"router '{router_key}': staged target topk {int(target.shape[1])} "
+                               f"!= router topk {b.topk}")
+        b.replay.set_target_indices(target)
+        b.replay.set_router_replay_action(RouterReplayAction.REPLAY_FORWARD)
+        m.installed[router_key] = (m.active, ci)

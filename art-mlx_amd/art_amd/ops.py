@@ -50,7 +50,8 @@ def router_replay(logits: torch.Tensor, target, status: torch.Tensor | None = No
     A target carrying ``table`` and ``rows`` (a device route table and row map,
     e.g. ``routing_replay.DeviceReplayTarget``) replays ``table[rows[t]]``."""
     if hasattr(target, "table") and hasattr(target, "rows"):
-        return router_replay_rows(logits, target.table, target.rows, status)
+        return router_replay_rows(logits, target.table, target.rows, status,
+                                  extra=getattr(target, "extra", None))
     _cuda(logits, target)
     _need(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be fp32 [T, E]")
     _need(target.dim() == 2 and target.shape[0] == logits.shape[0], "target must be [T, k]")
@@ -68,10 +69,11 @@ def router_replay(logits: torch.Tensor, target, status: torch.Tensor | None = No
 
 
 def router_replay_rows(logits: torch.Tensor, table: torch.Tensor, rows: torch.Tensor,
-                       status: torch.Tensor | None = None):
-    """Replay ``table[rows[t]]`` (table int32 [N, k] and rows int32 [T] on the
-    device; a row outside [0, N) rejects the token's ids).  Returns (idx, w, status)."""
-    _cuda(logits, table, rows)
+                       status: torch.Tensor | None = None, *, extra: torch.Tensor | None = None):
+    """Replay ``table[rows[t]]`` for rows[t] >= 0 and ``extra[-rows[t] - 1]``
+    for rows[t] < 0 (tables int32 [N, k] / [X, k], rows int32 [T], on the
+    device; an entry outside both rejects the token's ids).  Returns (idx, w, status)."""
+    _cuda(logits, table, rows, extra)
     _need(logits.dtype == torch.float32 and logits.dim() == 2, "logits must be fp32 [T, E]")
     _need(table.dtype == torch.int32 and table.dim() == 2 and table.is_contiguous(),
           "table must be contiguous int32 [N, k]")
@@ -84,8 +86,13 @@ def router_replay_rows(logits: torch.Tensor, table: torch.Tensor, rows: torch.Te
     w = torch.empty((t, k), dtype=torch.float32, device=logits.device)
     if status is None:
         status = torch.zeros(1, dtype=torch.int32, device=logits.device)
-    call("art_moe_router_replay_rows", ptr(logits), ptr(table), table.shape[0], ptr(rows), t, e, k,
-         ptr(idx), ptr(w), ptr(status), stream_ptr(logits.device))
+    n_extra = 0
+    if extra is not None:
+        _need(extra.dtype == torch.int32 and extra.dim() == 2 and extra.is_contiguous()
+              and extra.shape[1] == table.shape[1], "extra must be contiguous int32 [X, k]")
+        n_extra = extra.shape[0]
+    call("art_moe_router_replay_rows", ptr(logits), ptr(table), table.shape[0], ptr(extra), n_extra,
+         ptr(rows), t, e, k, ptr(idx), ptr(w), ptr(status), stream_ptr(logits.device))
     return idx, w, status
 
 

@@ -101,11 +101,13 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(
 
 // Replay: lane j < k of the token's wave takes target[t, j].
 // The target row of token t is target[t, :] (int64), or, with a row map,
-// table[rows[t], :] (int32 [n_rows, k]; a row outside the table rejects all
-// k ids of the token).
+// table[rows[t], :] (int32 [n_rows, k]) for rows[t] >= 0 and
+// extra[-rows[t] - 1, :] (int32 [n_extra, k]) for rows[t] < 0; a row map
+// entry outside both tables rejects all k ids of the token.
 __global__ __launch_bounds__(256) void replay_kernel(
     const float *__restrict__ logits, const int64_t *__restrict__ target,
-    const int32_t *__restrict__ table, int64_t n_rows, const int32_t *__restrict__ rows,
+    const int32_t *__restrict__ table, int64_t n_rows, const int32_t *__restrict__ extra,
+    int64_t n_extra, const int32_t *__restrict__ rows,
     int64_t T, int E, int k, int32_t *__restrict__ idx, float *__restrict__ w,
     int32_t *__restrict__ status) {
   const int lane = lane_id();
@@ -116,7 +118,8 @@ __global__ __launch_bounds__(256) void replay_kernel(
   if (act) {
     if (rows) {
       const int64_t r = rows[t];
-      e = (r >= 0 && r < n_rows) ? (int64_t)table[r * k + lane] : -1;
+      if (r >= 0) e = r < n_rows ? (int64_t)table[r * k + lane] : -1;
+      else e = -r <= n_extra ? (int64_t)extra[(-r - 1) * k + lane] : -1;
     } else {
       e = target[t * k + lane];
     }
@@ -764,23 +767,25 @@ extern "C" int art_moe_router_replay(const float *logits, const int64_t *target,
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(logits && target && idx && w && status, "router_replay: null pointer");
   replay_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
-      logits, target, nullptr, 0, nullptr, T, E, k, idx, w, status);
+      logits, target, nullptr, 0, nullptr, 0, nullptr, T, E, k, idx, w, status);
   return check_launch("router_replay");
 }
 
 extern "C" int art_moe_router_replay_rows(const float *logits, const int32_t *table,
-                                          int64_t n_rows, const int32_t *rows, int64_t T,
-                                          int32_t E, int32_t k, int32_t *idx, float *w,
-                                          int32_t *status, void *stream) {
+                                          int64_t n_rows, const int32_t *extra, int64_t n_extra,
+                                          const int32_t *rows, int64_t T, int32_t E, int32_t k,
+                                          int32_t *idx, float *w, int32_t *status, void *stream) {
   clear_error();
-  ART_REQUIRE(T >= 0 && n_rows >= 0 && E >= 1, "router_replay_rows: need T, n_rows >= 0 and E >= 1");
+  ART_REQUIRE(T >= 0 && n_rows >= 0 && n_extra >= 0 && E >= 1,
+              "router_replay_rows: need T, n_rows, n_extra >= 0 and E >= 1");
   ART_REQUIRE(k >= 1 && k <= E && k <= kMaxK, "router_replay_rows: need 1 <= k <= min(E, 32) (k=%d)",
               k);
   if (T == 0) return ART_MOE_OK;
-  ART_REQUIRE(logits && rows && idx && w && status && (table || n_rows == 0),
+  ART_REQUIRE(logits && rows && idx && w && status && (table || n_rows == 0) &&
+                  (extra || n_extra == 0),
               "router_replay_rows: null pointer");
   replay_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
-      logits, nullptr, table, n_rows, rows, T, E, k, idx, w, status);
+      logits, nullptr, table, n_rows, extra, n_extra, rows, T, E, k, idx, w, status);
   return check_launch("router_replay_rows");
 }
 

@@ -105,20 +105,22 @@ int art_moe_router_replay(const float *logits, const int64_t *target, int64_t T,
                           int32_t E, int32_t k, int32_t *idx, float *w,
                           int32_t *status, void *stream);
 
-/* Routing replay from a device-resident route table: the target row of token
- * t is table[rows[t], :] (table int32 [n_rows, k], rows int32 [T]); a row
- * outside [0, n_rows) rejects all k ids of the token (each adds 1 to
- * *status).  Otherwise as art_moe_router_replay.  The controller uploads a
- * step's route table once and a micro's row map once, instead of a
- * host-gathered [T, k] target per router call.
+/* Routing replay from device-resident route tables: the target row of token
+ * t is table[rows[t], :] for rows[t] >= 0 (table int32 [n_rows, k]) and
+ * extra[-rows[t] - 1, :] for rows[t] < 0 (extra int32 [n_extra, k]: the
+ * synthetic rows of tokens without a captured route); a row map entry
+ * outside both rejects all k ids of the token (each adds 1 to *status).
+ * Otherwise as art_moe_router_replay.  The controller uploads a step's route
+ * table once and a micro's row map once (shared by every router), instead of
+ * a host-gathered [T, k] target per router call.
  * Replaces: the host gather + per-call copy of
  * MoeRoutingReplayController._explicit_target_for_router_call /
  * _stage_prepared_target (src/art/megatron/routing_replay.py:1437-1474,
  * 1530-1572). */
 int art_moe_router_replay_rows(const float *logits, const int32_t *table,
-                               int64_t n_rows, const int32_t *rows, int64_t T,
-                               int32_t E, int32_t k, int32_t *idx, float *w,
-                               int32_t *status, void *stream);
+                               int64_t n_rows, const int32_t *extra, int64_t n_extra,
+                               const int32_t *rows, int64_t T, int32_t E, int32_t k,
+                               int32_t *idx, float *w, int32_t *status, void *stream);
 
 /* Router backward through the renormalised softmax.  dp_part holds n_part
  * fp32 partial vectors of length M (stride M) whose sum is dL/dp per permuted

@@ -53,9 +53,11 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert b"E <= 1024" in lib.art_moe_last_error()
     rc = lib.art_moe_router_topk(null, 4, 8, 9, null, null, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
-    rc = lib.art_moe_router_replay_rows(null, null, 0, null, 4, 4, 8, null, null, null, null)
+    rc = lib.art_moe_router_replay_rows(null, null, 0, null, 0, null, 4, 4, 8, null, null, null,
+                                        null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"min(E, 32)" in lib.art_moe_last_error()
-    rc = lib.art_moe_router_replay_rows(null, null, 0, null, 4, 8, 2, null, null, null, null)
+    rc = lib.art_moe_router_replay_rows(null, null, 0, null, 0, null, 4, 8, 2, null, null, null,
+                                        null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"null pointer" in lib.art_moe_last_error()
     rc = lib.art_moe_grouped_gemm(null, 12, null, null, null, 12, 0, null, 0, 0, null, 0, null, 0,
                                   0, 0, null, 4, 16, 32, 12, 1.0, null, 32, 0, null)

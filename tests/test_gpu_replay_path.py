@@ -120,3 +120,82 @@ def test_topk_router_module_matches_oracle(device):
     sel = torch.softmax(lc.gather(1, idx), dim=1)
     (sel * gout.gather(1, idx)).sum().backward()
     torch.testing.assert_close(logits.grad.cpu(), lc.grad, rtol=1e-5, atol=1e-6)
+
+
+def test_device_targets_with_uidless_tokens_equal_host_targets(device, tmp_path):
+    """Tokens without a uid (negative) get synthetic rows; on the device path
+    they come from the per-call side table the row map addresses with
+    negative entries.  Two routers, two micros, two uid layouts: every
+    installed target equals the host path's, and both replay identically."""
+    from art_amd import ops
+    from art_amd.megatron import routing_replay as RR
+    from art_amd.megatron.router import TopKRouter
+
+    t, h, e, k = 512, 64, 32, 4
+    g = torch.Generator().manual_seed(7)
+    keys = ["chunk_00.layer_0000.mlp.router", "chunk_00.layer_0001.mlp.router"]
+
+    def call(sample):
+        idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)]).to(torch.int32)
+        return RR.RouterCallRoute(expert_indices=idx, expert_mask=torch.ones_like(idx, dtype=torch.bool),
+                                  num_experts=e, sample_index=sample)
+    steps = {0: RR.StepRoutes(routers={rk: RR.StepRouterRoutes(calls={0: call(0), 1: call(1)})
+                                       for rk in keys},
+                              global_token_uids=torch.arange(1000, 1000 + t, dtype=torch.int64))}
+    bundle = RR.MoeRoutingReplayBundle(topology=RR.ParallelTopology(tp=1, ep=1), num_steps=1,
+                                       max_topk=k, router_keys=keys, steps=steps)
+    bundle.to_dir(tmp_path)
+    bundle = RR.MoeRoutingReplayBundle.from_dir(tmp_path)
+
+    class Two(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.decoder = torch.nn.Module()
+            self.decoder.layers = torch.nn.ModuleList()
+            for _ in keys:
+                layer = torch.nn.Module()
+                layer.mlp = torch.nn.Module()
+                layer.mlp.router = TopKRouter(h, e, k, moe_enable_routing_replay=True, device=device)
+                self.decoder.layers.append(layer)
+
+    uid_sets = []
+    for micro in range(2):
+        a = 1000 + torch.randperm(t, generator=g)[:300]
+        a[torch.randperm(300, generator=g)[:17]] = -1          # tokens without a uid
+        b = a.flip(0).clone()
+        uid_sets.append({"attention": a, "gdn": b})
+    logits = [torch.randn(300, e, generator=g).to(device) for _ in range(2)]
+
+    def run(device_targets):
+        model = Two()
+        ctl = RR.MoeRoutingReplayController(bundle=bundle, strict=True, device=device,
+                                            device_targets=device_targets)
+        ctl.install_router_patches([model])
+        ctl.set_step(step_index=0, sample_index=[0, 1])
+        out = []
+        for micro in range(2):
+            ctl.begin_micro(micro, micro)
+            ctl.prepare_micro_targets(uid_sets[micro])
+            for layout in ("attention", "gdn"):
+                ctl.set_active_token_uid_key(layout)
+                for layer in model.decoder.layers:
+                    r = layer.mlp.router
+                    probs, rmap = r.routing(logits[micro])
+                    tgt = r.router_replay.target_topk_idx
+                    assert isinstance(tgt, RR.DeviceReplayTarget) == device_targets
+                    ids = tgt.materialize() if device_targets else tgt
+                    out.append((ids.cpu(), probs.detach().cpu(), int(r.last_status.item())))
+        ctl.finalize_step()
+        ctl.remove_router_patches()
+        return out
+
+    host, dev = run(False), run(True)
+    assert len(host) == len(dev) == 8
+    for (hi, hp, hs), (di, dp, ds) in zip(host, dev):
+        assert torch.equal(hi, di) and torch.equal(hp, dp) and hs == ds == 0
+    # the synthetic rows follow the stdlib formula: seed (step+1)*1_000_003 + (call+1)*97_003
+    import random
+    a = uid_sets[0]["attention"]
+    p = int(torch.nonzero(a < 0)[0])
+    want = random.Random(1 * 1_000_003 + 1 * 97_003 + (p + 1) * 1_299_709).sample(range(e), k)
+    assert host[0][0][p].tolist() == want

@@ -261,3 +261,25 @@ def test_router_replay_rows_equals_gathered_target(device):
     assert torch.equal(idx_r.cpu(), idx_t.cpu()) and torch.equal(w_r.cpu(), w_t.cpu())
     assert int(st_r.item()) == int(st_t.item()) == 2 * k + 1
     assert (idx_r[3] == -1).all() and (idx_r[10] == -1).all() and int(idx_r[2999, 1]) == -1
+
+
+def test_router_replay_rows_reads_the_side_table_for_negative_rows(device):
+    """rows[t] < 0 replays extra[-rows[t] - 1] (the synthetic rows of tokens
+    without a captured route); entries past the side table are rejected."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(22)
+    n, x, t, e, k = 300, 5, 200, 64, 8
+    table = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)]).to(torch.int32)
+    extra = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(x)]).to(torch.int32)
+    rows = torch.randint(0, n, (t,), generator=g, dtype=torch.int32)
+    rows[[0, 17, 60, 199]] = torch.tensor([-1, -5, -3, -6], dtype=torch.int32)   # -6: past extra
+    logits = torch.randn(t, e, generator=g)
+    idx, w, st = ops.router_replay_rows(logits.to(device), table.to(device), rows.to(device),
+                                        extra=extra.to(device))
+    tgt = torch.where(rows.unsqueeze(1) >= 0, table[rows.clamp(0, n - 1).long()],
+                      extra[(-rows - 1).clamp(0, x - 1).long()]).long()
+    tgt[199] = -1
+    idx_t, w_t, st_t = ops.router_replay(logits.to(device), tgt.to(device))
+    assert torch.equal(idx.cpu(), idx_t.cpu()) and torch.equal(w.cpu(), w_t.cpu())
+    assert int(st.item()) == int(st_t.item()) == k
+    assert idx[17].tolist() == extra[4].tolist() and idx[0].tolist() == extra[0].tolist()

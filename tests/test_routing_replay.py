@@ -402,9 +402,9 @@ def test_controller_legacy_call_order_without_micro_metadata():
     b = bundle_of(calls, 2)
     c = controller(b, Chunk())
     c.set_step(step_index=0, sample_index=[1], global_grad_accumulation_sequences=2)
-    assert c._cursors[KEY].sequence == [2, 3]
+    assert c.call_plan(KEY) == [2, 3]
     c.set_step(step_index=0, sample_index=[0, 1], global_grad_accumulation_sequences=2)
-    assert c._cursors[KEY].sequence == [0, 1, 2, 3]
+    assert c.call_plan(KEY) == [0, 1, 2, 3]
     with pytest.raises(RuntimeError, match="not divisible"):
         c.set_step(step_index=0, sample_index=[0], global_grad_accumulation_sequences=3)
     with pytest.raises(RuntimeError, match="lacks sample metadata"):
