@@ -72,6 +72,8 @@ struct NTArgs {
   bf16 *dy1;          // bwd out [M][2F]
   float *dp_part;     // bwd out [ceil(F/128)][M]
   int64_t M;
+  int sched;  // tile schedule bits (see the tile loop of gemm_nt_kernel); bit 2: skip
+              // the row blocks past a tile's valid rows
 };
 
 typedef __attribute__((address_space(3))) void *lds_void_ptr;
@@ -128,13 +130,17 @@ __device__ __forceinline__ int chunk_swz(int r) {
 }
 
 // One stage of operand DMA for this wave: A_PW blocks of A rows, B_PW of B rows.
+// A blocks whose first row is >= a_blocks * RPB (past the tile's valid rows)
+// are skipped when a_blocks says so (callers pass a huge value otherwise).
 template <int A_PW, int B_PW, int A_BYTES>
 __device__ __forceinline__ void issue_stage(char *st, int wave, const char *abase,
                                             const char *bbase, const uint32_t (&aoff)[A_PW],
-                                            const uint32_t (&boff)[B_PW], uint32_t sh) {
+                                            const uint32_t (&boff)[B_PW], uint32_t sh,
+                                            int a_blocks) {
 #pragma unroll
   for (int i = 0; i < A_PW; ++i)
-    dma16((const bf16 *)(abase + (aoff[i] + sh)), st + (wave * A_PW + i) * 1024);
+    if (wave * A_PW + i < a_blocks)
+      dma16((const bf16 *)(abase + (aoff[i] + sh)), st + (wave * A_PW + i) * 1024);
 #pragma unroll
   for (int i = 0; i < B_PW; ++i)
     dma16((const bf16 *)(bbase + (boff[i] + sh)), st + A_BYTES + (wave * B_PW + i) * 1024);
@@ -162,11 +168,13 @@ __device__ __forceinline__ int b_source_row(int r, int nt, int N, int F) {
 template <int A_PW, int B_PW, int A_BYTES, int BK = 64>
 __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, const char *abase,
                                                  const char *bbase, const uint32_t (&aoff)[A_PW],
-                                                 const uint32_t (&boff)[B_PW], int kb, int klim) {
+                                                 const uint32_t (&boff)[B_PW], int kb, int klim,
+                                                 int a_blocks) {
   constexpr int CPR = BK / 8, RPB = 64 / CPR;
 #pragma unroll
   for (int i = 0; i < A_PW; ++i) {
     const int bi = wave * A_PW + i;
+    if (bi >= a_blocks) continue;
     const int ch = (lane % CPR) ^ chunk_swz<BK>(bi * RPB + lane / CPR);
     const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
     dma16((const bf16 *)(abase + (aoff[i] + (uint32_t)(off * 2))), st + bi * 1024);
@@ -181,11 +189,13 @@ __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, c
 }
 
 // MFMA operands of one 16-wide k step from a swizzled stage (rows of BK bf16).
+// Row blocks i >= tmv (no valid row) are not read.
 template <int TM, int TN, int WTM, int WTN, int A_BYTES, int BK = 64>
 __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int wn, int lrow, int lk,
-                                           bf16x8 (&af)[TM], bf16x8 (&bfv)[TN]) {
+                                           bf16x8 (&af)[TM], bf16x8 (&bfv)[TN], int tmv = TM) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    if (i >= tmv) continue;
     const int r = wm * WTM + i * 32 + lrow;
     af[i] = *(const bf16x8 *)(st + r * (2 * BK) + (((kk * 2 + lk) ^ chunk_swz<BK>(r)) << 4));
   }
@@ -243,9 +253,11 @@ __device__ __forceinline__ bf16x8 dequant8(uint2 q, const float (&sc)[8]) {
 template <int TM, int TN, int WTM, int WTN, int A_BYTES, int BQ8>
 __device__ __forceinline__ void load_frags8(const char *st, int kk, int wm, int wn, int lrow, int lk,
                                             bf16x8 (&af)[TM], bf16x8 (&bfv)[TN],
-                                            const float (&bsc)[TN], const float *ksc) {
+                                            const float (&bsc)[TN], const float *ksc,
+                                            int tmv = TM) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    if (i >= tmv) continue;
     const int r = wm * WTM + i * 32 + lrow;
     af[i] = *(const bf16x8 *)(st + r * 128 + (((kk * 2 + lk) ^ swz(r)) << 4));
   }
@@ -323,13 +335,16 @@ __device__ __forceinline__ bf16x8 scale_frag(bf16x8 v, float s) {
 // fp16 MFMA; otherwise bfloat16).
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// Row blocks i >= tmv hold no valid row of the tile: their MFMAs are skipped
+// (tmv is wave-uniform, so each test is one scalar branch).
 template <int TM, int TN, bool F16 = false>
 __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&af)[TM],
-                                         const bf16x8 (&bfv)[TN]) {
+                                         const bf16x8 (&bfv)[TN], int tmv = TM) {
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      if (i >= tmv) continue;
       if constexpr (F16)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bfv[j]),
                                                            __builtin_bit_cast(f16x8, af[i]),
@@ -397,13 +412,36 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES];
   float *sRed = (float *)(smem + LDS_BYTES);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is uniform across the wave: readfirstlane tells the
+  // compiler so, keeping every role test and loop counter that depends on it
+  // in scalar registers (plain scalar branches instead of exec-mask control
+  // flow in the k-loop).
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int lrow = lane & 31, lk = lane >> 5;
   const int n_tiles = (p.N + BN - 1) / BN;
   const int total = p.tile_off[p.E] * n_tiles;
+  // Tile schedule.  Workgroups are dispatched round-robin over the 8 XCDs
+  // (blockIdx % 8), each with its own L2.  Default: round r gives XCD x the
+  // 32-tile window [r*nb + x*nb/8, ...).  p.sched bit 0: XCD x owns one
+  // contiguous eighth of the tile list for the whole launch and walks it
+  // nb/8 tiles at a time, so a round continues where the XCD's previous one
+  // stopped.  Bit 1: inside an expert, column tiles outer and row tiles
+  // inner, so the row tiles that read one weight column slice run side by side.
   const int nb = gridDim.x;
-  const int lb = (nb % 8 == 0) ? ((blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3)) : blockIdx.x;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per_x = nb >> 3;
+  int t_begin = blockIdx.x, t_step = nb, t_end = total;
+  if (nb % 8 == 0) {
+    if (p.sched & 1) {
+      const int span = (total + 7) / 8;
+      t_begin = xcd * span + slot;
+      t_step = per_x;
+      t_end = min(total, (xcd + 1) * span);
+    } else {
+      t_begin = xcd * per_x + slot;
+    }
+  }
   const int nk_main = (p.K + KPS - 1) / KPS;
   const int nk = nk_main + (p.kt + BK - 1) / BK;
   const int nk_full = p.K / KPS;  // full k-tiles of the base product
@@ -411,18 +449,40 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   // physical chunk lane%CPR, holding logical chunk (lane%CPR) ^ chunk_swz(row).
   const int drow = lane / CPR, dch = lane % CPR;
 
-  for (int tile = lb; tile < total; tile += nb) {
-    const int mt = tile / n_tiles, nt = tile - mt * n_tiles;
+  for (int tile = t_begin; tile < t_end; tile += t_step) {
+    // expert e of the tile: the last e whose first tile is <= tile (empty
+    // experts share their successor's start and are skipped by taking the last)
+    const bool ntm = (p.sched & 2) != 0;
+    const int key = ntm ? tile : tile / n_tiles;
+    const int scale = ntm ? n_tiles : 1;
     int lo = 0, hi = p.E;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (p.tile_off[mid] <= mt) lo = mid; else hi = mid;
+      if (p.tile_off[mid] * scale <= key) lo = mid; else hi = mid;
     }
     const int e = lo;
+    int mt, nt;
+    if (ntm) {
+      const int rows_e = p.tile_off[e + 1] - p.tile_off[e];
+      const int li = tile - p.tile_off[e] * n_tiles;
+      nt = li / rows_e;
+      mt = p.tile_off[e] + (li - nt * rows_e);
+    } else {
+      mt = key;
+      nt = tile - mt * n_tiles;
+    }
     const int m0 = p.seg_off[e] + (mt - p.tile_off[e]) * BM;
     // Rows of the segment, never past the M rows of A / C (a segment table
     // whose counts sum to more than M must not send the kernel past them).
     const int m_end = min(p.seg_off[e + 1], (int)p.M);
+    // Valid rows of the tile: this wave's row blocks that hold any (tmv) and,
+    // with a 2-stage ring (every wait drains all DMA: vmcnt(0)), the A DMA
+    // blocks that hold any (a_blocks); the rest is neither loaded nor
+    // multiplied.  Rows past m_end are never stored, and each output row
+    // depends on its own A row only, so what those LDS rows hold is moot.
+    const int vrows = (p.sched & 4) ? m_end - m0 : BM;
+    const int tmv = min(max((vrows - wm * WTM + 31) >> 5, 0), TM);
+    const int a_blocks = (STAGES == 2 && !A8) ? (vrows + RPB - 1) / RPB : (1 << 30);
 
     // Source rows of this lane's DMA slots (clamped into the segment / N), as
     // 32-bit byte offsets from wave-uniform bases (the host checks that every
@@ -497,7 +557,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     }                                                                                         \
     issue_stage_tail<A_PW, B_PW, A_BYTES, BK>(                                                \
         smem + ((ks) % STAGES) * STAGE_BYTES, wave, lane, (const char *)p.t,                  \
-        (const char *)(p.l + (int64_t)e * p.l_es), toff_, loff_, ((ks) - nk_main) * BK, p.kt); \
+        (const char *)(p.l + (int64_t)e * p.l_es), toff_, loff_, ((ks) - nk_main) * BK, p.kt, \
+        a_blocks);                                                                            \
   } while (0)
 
 #define ART_ISSUE(ks)                                                                         \
@@ -512,12 +573,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
                  st_ + A_BYTES + B_BYTES);                                                    \
       } else {                                                                                \
         issue_stage<A_PW, B_PW, A_BYTES>(st_, wave, abase, bbase, aoff, boff,                 \
-                                         (uint32_t)((ks) * BK * 2));                          \
+                                         (uint32_t)((ks) * BK * 2), a_blocks);                \
       }                                                                                       \
     } else if ((ks) < nk_main) {                                                              \
       if constexpr (BQ8 == B_BF16)                                                            \
         issue_stage_tail<A_PW, B_PW, A_BYTES, BK>(st_, wave, lane, abase, bbase, aoff, boff,  \
-                                                  (ks) * BK, p.K);                            \
+                                                  (ks) * BK, p.K, a_blocks);                  \
     } else {                                                                                  \
       ART_ISSUE_LORA(ks);                                                                     \
     }                                                                                         \
@@ -581,20 +642,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       bf16x8 af0[TM], bf0[TN], af1[TM], bf1[TN];
       if (nk_full > 0) {
         ART_STAGE_IN(0);
-        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem, 0, wm, wn, lrow, lk, af0, bf0);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem, 0, wm, wn, lrow, lk, af0, bf0, tmv);
       }
       for (int ks = 0; ks < nk_full; ++ks) {
         const char *st = smem + (ks % STAGES) * STAGE_BYTES;
-        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, 1, wm, wn, lrow, lk, af1, bf1);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, 1, wm, wn, lrow, lk, af1, bf1, tmv);
         __builtin_amdgcn_sched_barrier(0);
-        mma_step<TM, TN, F16>(acc, af0, bf0);
+        mma_step<TM, TN, F16>(acc, af0, bf0, tmv);
         __builtin_amdgcn_sched_barrier(0);
         if (ks + 1 < nk) ART_STAGE_IN_STAGGERED(ks + 1);
         if (ks + 1 < nk_full)
           load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(smem + ((ks + 1) % STAGES) * STAGE_BYTES, 0,
-                                                    wm, wn, lrow, lk, af0, bf0);
+                                                    wm, wn, lrow, lk, af0, bf0, tmv);
         __builtin_amdgcn_sched_barrier(0);
-        mma_step<TM, TN, F16>(acc, af1, bf1);
+        mma_step<TM, TN, F16>(acc, af1, bf1, tmv);
         __builtin_amdgcn_sched_barrier(0);
         if (late_issue && ks + STAGES < nk) ART_ISSUE(ks + STAGES);
       }
@@ -610,36 +671,36 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #define ART_FENCE() __builtin_amdgcn_sched_barrier(0)
       if (W8) {
         const float *ksc = (const float *)(st + A_BYTES + B_BYTES);
-        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 0, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
-        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 1, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 0, wm, wn, lrow, lk, af0, bf0, bsc, ksc, tmv);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 1, wm, wn, lrow, lk, af1, bf1, bsc, ksc, tmv);
         ART_FENCE();
-        mma_step<TM, TN, F16>(acc, af0, bf0);
+        mma_step<TM, TN, F16>(acc, af0, bf0, tmv);
         ART_FENCE();
-        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 2, wm, wn, lrow, lk, af0, bf0, bsc, ksc);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 2, wm, wn, lrow, lk, af0, bf0, bsc, ksc, tmv);
         ART_FENCE();
-        mma_step<TM, TN, F16>(acc, af1, bf1);
+        mma_step<TM, TN, F16>(acc, af1, bf1, tmv);
         ART_FENCE();
         if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
         ART_FENCE();
-        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 3, wm, wn, lrow, lk, af1, bf1, bsc, ksc);
+        load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 3, wm, wn, lrow, lk, af1, bf1, bsc, ksc, tmv);
       } else {
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0);
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0, tmv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1, tmv);
         ART_FENCE();
-        mma_step<TM, TN, F16>(acc, af0, bf0);
+        mma_step<TM, TN, F16>(acc, af0, bf0, tmv);
         ART_FENCE();
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0, tmv);
         ART_FENCE();
-        mma_step<TM, TN, F16>(acc, af1, bf1);
+        mma_step<TM, TN, F16>(acc, af1, bf1, tmv);
         ART_FENCE();
         if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
         ART_FENCE();
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1);
+        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1, tmv);
       }
       ART_FENCE();
-      mma_step<TM, TN, F16>(acc, af0, bf0);
+      mma_step<TM, TN, F16>(acc, af0, bf0, tmv);
       ART_FENCE();
-      mma_step<TM, TN, F16>(acc, af1, bf1);
+      mma_step<TM, TN, F16>(acc, af1, bf1, tmv);
 #undef ART_FENCE
     }
     }
@@ -654,14 +715,14 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       const int nkk = (klim - kb) >= BK ? BK / 16 : (klim - kb) / 16;
       for (int kk = 0; kk < nkk; ++kk) {
         bf16x8 af[TM], bfv[TN];
-        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, kk, wm, wn, lrow, lk, af, bfv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, kk, wm, wn, lrow, lk, af, bfv, tmv);
         if (A8) {  // LoRA terms join the fp8 accumulators pre-divided by the row scales
 #pragma unroll
           for (int i = 0; i < TM; ++i) af[i] = scale_frag(af[i], 1.0f / asc[i]);
 #pragma unroll
           for (int j = 0; j < TN; ++j) bfv[j] = scale_frag(bfv[j], 1.0f / bsc[j]);
         }
-        mma_step<TM, TN, F16>(acc, af, bfv);
+        mma_step<TM, TN, F16>(acc, af, bfv, tmv);
       }
     }
 #undef ART_STAGE_IN
@@ -884,6 +945,17 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 }
 
 
+// Tile schedule bits of gemm_nt_kernel, ART_MOE_GEMM_SCHED=<0..7> (read once).
+static int tile_sched() {
+  static int v = -1;
+  if (v < 0) {
+    const char *e = getenv("ART_MOE_GEMM_SCHED");
+    const int x = (e && *e) ? atoi(e) : 7;
+    v = (x >= 0 && x <= 7) ? x : 7;
+  }
+  return v;
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64,
           bool F16 = false>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
@@ -904,6 +976,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   NTArgs p = a;
   p.seg_off = seg;
   p.tile_off = seg + (1 + bmi) * (a.E + 1);
+  p.sched = tile_sched();
   const int n_tiles = (a.N + BN - 1) / BN;
   const int64_t max_tiles = ((M + BM - 1) / BM + a.E) * (int64_t)n_tiles;
   int64_t grid = (int64_t)device_cu_count() * occ;
