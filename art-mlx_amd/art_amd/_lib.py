@@ -70,10 +70,13 @@ SIGNATURES = {
                                     _I64, _I64, _I32, _P, _I32, _I64, _I32, _I32, _F, _P, _I64,
                                     _I32, _P]),
     "art_moe_fc1_swiglu": (_I32, [_P, _I64, _P, _P, _P, _P, _I32, _P, _I64, _P, _I32, _P, _I32, _I64,
-                                  _I32, _I32, _P, _P, _P, _P]),
+                                  _I32, _I32, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I32, _P]),
+    "art_moe_lora_epilogue_parts": (_I32, [_I32, _I32, _I32]),
+    "art_moe_sum_parts": (_I32, [_P, _I32, _I64, _I32, _P, _I32, _P, _I64, _P]),
     "art_moe_dgrad_swiglu_parts": (_I32, [_I32]),
     "art_moe_fc2_dgrad_swiglu": (_I32, [_P, _I64, _P, _P, _P, _P, _I32, _P, _I64, _P, _I32, _P, _I32,
-                                        _I64, _I32, _I32, _P, _P, _P, _P, _P]),
+                                        _I64, _I32, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32,
+                                        _P, _I32, _P]),
     "art_moe_grouped_wgrad": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32, _F,
                                      _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _I32, _P,
                                      _SZ, _P]),

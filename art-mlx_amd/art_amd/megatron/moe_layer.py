@@ -14,13 +14,13 @@ forward
   3 dispatch plan          counts, segment table, dest, row->token, row->prob
   4 LoRA projection        t1 = x[row] [A_g | A_u]               (rows gathered)
   5 FC1 + LoRA + SwiGLU    y1 = x[row] W1^T + t1 L1^T ; h = silu(g) u p
-  6 LoRA projection        t2 = h A_d
+  6 LoRA projection        t2 = h A_d (in FC1's epilogue: partials + sum)
   7 FC2 + LoRA             y2 = h W2^T + t2 (s_d B_d)^T
   8 combine                y[t] = sum_j y2[dest[t, j]]
 backward
   1 g2  = s_d dy[row] B_d^T
   2 FC2 dgrad + SwiGLU bwd dy1, dp  (dh = dy[row] W2 + g2 A_d^T)
-  3 g1  = [s_g dg B_g^T | s_u du B_u^T]
+  3 g1  = [s_g dg B_g^T | s_u du B_u^T] (in the FC2-dgrad epilogue: partials + sum)
   4 FC1 dgrad              dx_perm = dy1 W1 + g1 [A_g | A_u]^T
   5 router bwd             dl = w (dw - <w, dw>)
   6 un-permute + router dx dx[t] = sum_j dx_perm[dest[t,j]] + sum_j dl[t,j] W_r[idx[t,j]]
@@ -35,8 +35,15 @@ from typing import Any
 
 import torch
 
+import os
+
 from .. import ops
 from .kernels.grouped_lora_hip import padded_rank
+
+# The LoRA projections of h (forward) and dy1 (backward) run inside the
+# epilogues that produce h and dy1 (fp32 partials per column tile, then one
+# fixed-order sum); ART_MOE_FUSE_PROJ=0 runs them as separate narrow products.
+FUSE_PROJECTIONS = os.environ.get("ART_MOE_FUSE_PROJ", "1") != "0"
 
 
 @dataclass
@@ -236,14 +243,20 @@ class _MoELoRALayerFn(torch.autograd.Function):
         m = t * k
         rows = plan.row_token
         t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
+        proj = a2p if FUSE_PROJECTIONS else None
         if base.act_fp8:   # W8A8: x per token, h per routed row, scales in the epilogues
             xq, xs = ops.quantize_rows_fp8(x)
-            y1, h = ops.fc1_swiglu(xq, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
-                                   tl=t1, l1=l1, w1_scale=base.w1_scale, a_scale=xs)
+            out = ops.fc1_swiglu(xq, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
+                                 tl=t1, l1=l1, w1_scale=base.w1_scale, a_scale=xs, proj=proj)
         else:
-            y1, h = ops.fc1_swiglu(x, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
-                                   tl=t1, l1=l1, w1_scale=base.w1_scale)
-        t2 = ops.grouped_gemm(h, a2p, plan.seg, e, m=m)
+            out = ops.fc1_swiglu(x, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
+                                 tl=t1, l1=l1, w1_scale=base.w1_scale, proj=proj)
+        if proj is not None:         # t2 = h A_d from the FC1 epilogue's partials
+            y1, h, part = out
+            t2 = ops.sum_parts(part, plan.seg)
+        else:
+            y1, h = out
+            t2 = ops.grouped_gemm(h, a2p, plan.seg, e, m=m)
         if base.act_fp8:
             hq, hs = ops.quantize_rows_fp8(h, seg=plan.seg)
             y2 = ops.grouped_gemm(hq, base.w2, plan.seg, e, m=m, tl=t2, l=l2,
@@ -295,18 +308,25 @@ class _MoELoRALayerFn(torch.autograd.Function):
         ops.pack(*items)
         # FC2 data gradient with the SwiGLU backward in its epilogue
         g2 = ops.grouped_gemm(dy, bdp, seg, e, m=m, a_rows=rows, alpha=sd)
+        proj = gb if FUSE_PROJECTIONS else None
+        split = 0 if fused_gu else rpg     # the dual adapter's gb is block-diagonal
         if base.act_fp8:
             # W8A8: the weights' per-k scales (the FC2 / FC1 output channels)
             # are folded into the gathered dy rows and the dy1 rows, which are
             # then quantised per routed row
             dyq, dys = ops.quantize_rows_fp8(dy, rows=rows, seg=seg, col_scale=base.w2_scale, m=m)
-            dy1, dp_part = ops.fc2_dgrad_swiglu(dyq, base.w2t, seg, e, y1, row_prob, m=m,
-                                                tl=g2, l2=adp, a_scale=dys)
+            out = ops.fc2_dgrad_swiglu(dyq, base.w2t, seg, e, y1, row_prob, m=m,
+                                       tl=g2, l2=adp, a_scale=dys, proj=proj, proj_split=split)
         else:
-            dy1, dp_part = ops.fc2_dgrad_swiglu(dy, base.w2t, seg, e, y1, row_prob, m=m,
-                                                a_rows=rows, tl=g2, l2=adp,
-                                                w2_scale=base.w2_scale)
-        g1 = ops.grouped_gemm(dy1, gb, seg, e, m=m)
+            out = ops.fc2_dgrad_swiglu(dy, base.w2t, seg, e, y1, row_prob, m=m,
+                                       a_rows=rows, tl=g2, l2=adp,
+                                       w2_scale=base.w2_scale, proj=proj, proj_split=split)
+        if proj is not None:         # g1 = dy1 [[s_g B_g, 0], [0, s_u B_u]]^T from the epilogue
+            dy1, dp_part, part = out
+            g1 = ops.sum_parts(part, seg)
+        else:
+            dy1, dp_part = out
+            g1 = ops.grouped_gemm(dy1, gb, seg, e, m=m)
         if base.act_fp8:
             dy1q, dy1s = ops.quantize_rows_fp8(dy1, seg=seg, col_scale=base.w1_scale, m=m)
             dx_perm = ops.grouped_gemm(dy1q, base.w1t, seg, e, m=m, tl=g1, l=a1cat, a_scale=dy1s)

@@ -276,14 +276,46 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
     return out
 
 
+def _projection(pj: torch.Tensor | None, product: int, f: int, fmt: int, m: int, num_experts: int,
+                width: int, dev):
+    """(pointer args, partial buffer) of a fused LoRA projection operand
+    ``pj`` [E, R, >= width] bf16 (R a multiple of 16), or zeros without one."""
+    if pj is None:
+        return (None, 0, 0, 0, None, 0), None
+    _need(pj.dtype == torch.bfloat16 and pj.dim() == 3 and pj.shape[0] == num_experts
+          and pj.shape[2] >= width and pj.shape[1] % 16 == 0 and pj.stride(2) == 1,
+          f"projection operand must be bf16 [E, R (multiple of 16), >= {width}]")
+    tiles = int(_lib.load().art_moe_lora_epilogue_parts(product, f, fmt))
+    part = torch.empty((tiles, m, pj.shape[1]), dtype=torch.float32, device=dev)
+    return (ptr(pj), pj.stride(0), pj.stride(1), pj.shape[1], ptr(part), tiles), part
+
+
+def sum_parts(part: torch.Tensor, seg: torch.Tensor | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [M, N] = sum over t of the fp32 partials ``part`` [T, M, N] in t
+    order (rows past the segments of ``seg``: 0)."""
+    _cuda(part, seg, out)
+    t, m, n = part.shape
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=part.device)
+    e = _lib.experts_of_seg(seg) if seg is not None else 0
+    call("art_moe_sum_parts", ptr(part.contiguous()), t, m, n, ptr(seg), e, ptr(out),
+         _rowmajor(out, "out"), stream_ptr(part.device))
+    return out
+
+
 def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts: int,
                row_prob: torch.Tensor, *, m: int, a_rows: torch.Tensor | None = None,
                tl: torch.Tensor | None = None, l1: torch.Tensor | None = None,
-               w1_scale: torch.Tensor | None = None, a_scale: torch.Tensor | None = None):
+               w1_scale: torch.Tensor | None = None, a_scale: torch.Tensor | None = None,
+               proj: torch.Tensor | None = None):
     """(y1 [M,2F], h [M,F]) = FC1 (+LoRA) then weighted SwiGLU, fused.
     ``w1`` is bf16, or fp8 e4m3fn with per-row scales ``w1_scale`` [E, 2F];
-    with ``a_scale`` the activations are fp8 too (W8A8, see grouped_gemm)."""
-    _cuda(a, w1, seg, row_prob, a_rows, tl, l1, w1_scale, a_scale)
+    with ``a_scale`` the activations are fp8 too (W8A8, see grouped_gemm).
+    With ``proj`` [E, R, F] (the down adapter's A^T, rank padded to 16) the
+    epilogue also projects h: returns (y1, h, part), ``part`` the fp32
+    partials [tiles, M, R] whose ``sum_parts`` is h @ proj[e]^T per segment."""
+    _cuda(a, w1, seg, row_prob, a_rows, tl, l1, w1_scale, a_scale, proj)
     e, f2, k = w1.shape
     f = f2 // 2
     _need(w1.is_contiguous(), "w1 must be contiguous [E, 2F, K]")
@@ -296,12 +328,13 @@ def fc1_swiglu(a: torch.Tensor, w1: torch.Tensor, seg: torch.Tensor, num_experts
         ldt = _rowmajor(tl, "Tl")
     y1 = torch.empty((m, f2), dtype=torch.bfloat16, device=a.device)
     h = torch.empty((m, f), dtype=torch.bfloat16, device=a.device)
+    pj_args, part = _projection(proj, 0, f, fmt, m, num_experts, f, a.device)
     call("art_moe_fc1_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(a_scale), ptr(w1),
          ptr(wsc), fmt,
          ptr(tl), ldt,
-         ptr(l1), kt, ptr(seg), num_experts, m, f, k, ptr(row_prob), ptr(y1), ptr(h),
+         ptr(l1), kt, ptr(seg), num_experts, m, f, k, ptr(row_prob), ptr(y1), ptr(h), *pj_args,
          stream_ptr(a.device))
-    return y1, h
+    return (y1, h) if part is None else (y1, h, part)
 
 
 def dgrad_swiglu_parts(f: int) -> int:
@@ -312,12 +345,18 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
                      y1: torch.Tensor, row_prob: torch.Tensor, *, m: int,
                      a_rows: torch.Tensor | None = None, tl: torch.Tensor | None = None,
                      l2: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
-                     a_scale: torch.Tensor | None = None):
+                     a_scale: torch.Tensor | None = None, proj: torch.Tensor | None = None,
+                     proj_split: int = 0):
     """(dy1 [M,2F] bf16, dp_part [n_parts, M] fp32) of the FC2 dgrad + SwiGLU backward.
+    With ``proj`` [E, R, 2F] (the FC1 adapter's scaled B, rank padded to 16)
+    the epilogue also projects dy1: returns (dy1, dp_part, part), ``part`` the
+    fp32 partials whose ``sum_parts`` is dy1 @ proj[e]^T per segment.  With
+    ``proj_split`` S > 0, ``proj`` is block-diagonal: rows < S see only the
+    first F columns, rows >= S only the last F (the rest is never read).
     ``w2t`` is bf16, or fp8 e4m3fn with the FC2 row scales ``w2_scale`` [E, K].
     W8A8 (``a_scale``): ``a`` is fp8 with the FC2 row scales already folded in
     (``quantize_rows_fp8(..., col_scale=w2_scale)``) and ``w2_scale`` is None."""
-    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2, w2_scale, a_scale)
+    _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2, w2_scale, a_scale, proj)
     e, f, k = w2t.shape
     _need(w2t.is_contiguous(), "w2t must be contiguous [E, F, K]")
     fmt, wsc, _ = _weight_format(w2t, w2_scale, True, a_scale)
@@ -330,12 +369,14 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
         ldt = _rowmajor(tl, "Tl")
     dy1 = torch.empty((m, 2 * f), dtype=torch.bfloat16, device=a.device)
     dp_part = torch.empty((dgrad_swiglu_parts(f), m), dtype=torch.float32, device=a.device)
+    pj_args, part = _projection(proj, 1, f, fmt, m, num_experts, 2 * f, a.device)
+    pj_args = pj_args[:4] + (proj_split if proj is not None else 0,) + pj_args[4:]
     call("art_moe_fc2_dgrad_swiglu", ptr(a), _rowmajor(a, "A"), ptr(a_rows), ptr(a_scale), ptr(w2t),
          ptr(wsc),
          fmt, ptr(tl), ldt,
          ptr(l2), kt, ptr(seg), num_experts, m, f, k, ptr(y1), ptr(row_prob), ptr(dy1),
-         ptr(dp_part), stream_ptr(a.device))
-    return dy1, dp_part
+         ptr(dp_part), *pj_args, stream_ptr(a.device))
+    return (dy1, dp_part) if part is None else (dy1, dp_part, part)
 
 
 def quantize_rows_fp8(src: torch.Tensor, *, rows: torch.Tensor | None = None,

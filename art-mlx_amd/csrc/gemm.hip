@@ -30,6 +30,7 @@
 // The MFMA is issued with B as its first operand, so a lane's accumulators
 // hold 4 consecutive output columns of one row; epilogues pack them to bf16,
 // stage the tile through the (now idle) LDS ring and write 16-byte chunks.
+#include <stdio.h>
 #include <stdlib.h>
 
 #include "common.h"
@@ -74,6 +75,15 @@ struct NTArgs {
   int64_t M;
   int sched;  // tile schedule bits (see the tile loop of gemm_nt_kernel); bit 2: skip
               // the row blocks past a tile's valid rows
+  // LoRA projection of the epilogue's output tile (SwiGLU epilogues):
+  // pj_part[t][m][n] = sum over the tile's columns c of out[m][c] * pj_b[e][n][c]
+  // for column tile t, n < pj_n (fp32 partials, summed in tile order later).
+  const bf16 *pj_b;   // [E][pj_n][pj_ld] bf16 (nullptr: no projection)
+  int64_t pj_es;
+  int pj_ld;
+  int pj_n;
+  float *pj_part;     // [tiles][M][pj_n]
+  int pj_split;       // > 0: P is block-diagonal (n < split: first half only)
 };
 
 typedef __attribute__((address_space(3))) void *lds_void_ptr;
@@ -373,6 +383,101 @@ constexpr int epi2_groups(int tm, int bm, int bn, int lds_bytes) {
   return 0;
 }
 
+// LoRA projection of an epilogue tile staged in LDS (bf16 rows of 8-byte
+// units, unit u of staging row r at stg[r * UPR + (u ^ (r & UMASK))]):
+//   part[t][m0 + row_of(r)][n] = sum_g sum_{c < KC} T_g[r][c] * P[n][pcol_g + c]
+// over NREG staged regions g (region g's rows start at staging row
+// g * REG_ROWS; its P columns at pcol[g]), for the staging rows r < NR and
+// n < NQ; with split > 0, n < split takes region 0 only and n >= split
+// region 1 only (a block-diagonal P).  One v_mfma_f32_16x16x32_bf16 per
+// (16-row block, 16-column block, 32-wide k step), spread over the NW
+// waves: lane l takes row l % 16 of the block and k = 8 (l / 16) .. +7 for
+// both operands; D element v is row 4 (l / 16) + v, column l % 16.  Region
+// g's P columns at or past plim[g] (past the output width) count as zero.
+// P comes from the tile's slice in LDS (pj_lds: [NREG][NQ][KC] with the 16-
+// byte chunk c of row n at c ^ (n & 15), see load_proj_slice) or, when that
+// is null, straight from global memory.
+template <int KC, int UPR, int UMASK, int NREG, int REG_ROWS, int NR, int NW, typename RowOf>
+__device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_lds, const bf16 *P,
+                                              int ldp, const int (&pcol)[NREG],
+                                              const int (&plim)[NREG], int NQ, int split,
+                                              float *part, int64_t M, int m0, int m_end,
+                                              int wave, int lane, RowOf row_of) {
+  static_assert(KC % 32 == 0 && NR % 16 == 0, "projection tile");
+  constexpr int KS = KC / 32;                           // k steps per region
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int pairs = (NR / 16) * (NQ >> 4);
+  for (int pi = wave; pi < pairs; pi += NW) {
+    const int rb = pi / (NQ >> 4), nb = pi - rb * (NQ >> 4);
+    if (m0 + row_of(rb * 16) >= m_end) continue;   // block past the segment (rows ascend)
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int n = nb * 16 + l16;
+    const bf16 *prow = P + (int64_t)n * ldp;
+    const int g_lo = (split > 0 && NREG > 1 && nb * 16 >= split) ? 1 : 0;
+    const int g_hi = (split > 0 && NREG > 1 && nb * 16 < split) ? 1 : NREG;
+#pragma unroll
+    for (int g = 0; g < NREG; ++g) {
+      if (g < g_lo || g >= g_hi) continue;
+      const int r = g * REG_ROWS + rb * 16 + l16;
+      const char *brow = pj_lds ? pj_lds + (g * NQ + n) * (KC * 2) : nullptr;
+#pragma unroll
+      for (int k0 = 0; k0 < KS; k0 += 2) {
+        U4 a4[2], b4[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (k0 + j >= KS) continue;
+          const int kk = k0 + j;
+          const int u = kk * 8 + 2 * g4;               // first 8-byte unit of the lane's k run
+          const uint2 lo = stg[r * UPR + (u ^ (r & UMASK))];
+          const uint2 hi = stg[r * UPR + ((u + 1) ^ (r & UMASK))];
+          a4[j] = U4{lo.x, lo.y, hi.x, hi.y};
+          const int c = pcol[g] + kk * 32 + 8 * g4;
+          if (brow) b4[j] = *(const U4 *)(brow + (((kk * 4 + g4) ^ (n & 15)) << 4));
+          else b4[j] = *(const U4 *)(prow + (c < plim[g] ? c : pcol[g]));
+          if (c >= plim[g]) b4[j] = U4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          if (k0 + j >= KS) continue;
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a4[j]),
+                                                        __builtin_bit_cast(bf16x8, b4[j]), acc,
+                                                        0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = m0 + row_of(rb * 16 + 4 * g4 + v);
+      if (m < m_end) part[(int64_t)m * NQ + n] = acc[v];
+    }
+  }
+}
+
+// The tile's slice of the projection operand into LDS by DMA: region g,
+// row n, columns pcol[g] .. +KC (chunks past the row's end re-read its first
+// chunk; epi_lora_proj zeroes those columns).  16-byte chunk c of row n goes
+// to physical chunk c ^ (n & 15), so the 16 rows a half-wave reads at one
+// column land on distinct banks.
+template <int KC, int NREG, int NW>
+__device__ __forceinline__ void load_proj_slice(char *pj_lds, const bf16 *P, int ldp,
+                                                const int (&pcol)[NREG], const int (&plim)[NREG],
+                                                int NQ, int wave, int lane) {
+  constexpr int CPRO = KC / 8;                         // chunks per row
+  const int n_instr = NREG * NQ * CPRO / 64;           // 1 KB per DMA instruction
+  for (int ii = wave; ii < n_instr; ii += NW) {
+    const int ch = ii * 64 + lane;                     // physical chunk index in the slice
+    const int row = ch / CPRO, pc = ch - row * CPRO;   // row = g * NQ + n
+    const int g = row / NQ, n = row - g * NQ;
+    const int lc = pc ^ (n & 15);
+    int col = pcol[0];
+#pragma unroll
+    for (int gg = 0; gg < NREG; ++gg)
+      if (gg == g) col = pcol[gg] + lc * 8 < plim[gg] ? pcol[gg] + lc * 8 : pcol[gg];
+    __builtin_amdgcn_global_load_lds((const void *)(P + (int64_t)n * ldp + col),
+                                     (lds_void_ptr)(pj_lds + ii * 1024), 16, 0, 0);
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64,
           bool F16 = false>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
@@ -394,6 +499,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int G = W8 ? A_PW + B_PW8 : A_PW + B_PW;
   constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
   constexpr int RED_BYTES = EPI == EPI_SWIGLU_BWD ? WN * BM * 4 : 0;  // dp row partials
+  // SwiGLU products with one workgroup per CU anyway: what LDS is left holds
+  // the tile's slice of the LoRA projection operand (DMA'd with the first
+  // stages, read by the epilogue)
+  constexpr int PJ_SPARE = 160 * 1024 - STAGES * (BM * BK * 2 + BN * BK * 2 +
+                                                  (BQ8 == B_FP8_KSCALE ? BK * 4 : 0)) - RED_BYTES;
+  constexpr int PJ_BYTES = (EPI != EPI_STORE && STAGES * (BM + BN) * BK * 2 > 80 * 1024 && PJ_SPARE > 0)
+                               ? (PJ_SPARE / 1024) * 1024 : 0;
   constexpr int UMASK = (BN / 4 >= 32) ? 31 : (BN / 4 - 1);  // staging swizzle (8-byte units)
   static_assert(TM >= 1 && TN >= 1 && A_PW >= 1 && B_PW >= 1, "tile config");
   static_assert((BM / RPB) % NW == 0 && (BN / RPB) % NW == 0, "DMA blocks must split across waves");
@@ -402,15 +514,16 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   static_assert(EPI != EPI_SWIGLU_FWD || (TN % 2 == 0), "SwiGLU forward pairs gate/up blocks");
   static_assert(BM * BN * 2 <= LDS_BYTES, "epilogue staging must fit the LDS ring");
   static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 6, "vmcnt range");
-  static_assert(LDS_BYTES + RED_BYTES <= 160 * 1024, "LDS of one workgroup");
+  static_assert(LDS_BYTES + RED_BYTES + PJ_BYTES <= 160 * 1024, "LDS of one workgroup");
   static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
   constexpr int EPI2_NH = EPI == EPI_SWIGLU_BWD ? epi2_groups(TM, BM, BN, LDS_BYTES) : 1;
   static_assert(EPI2_NH >= 1, "SwiGLU backward staging (dg and du of a row group) must fit the LDS ring");
   static_assert(!W8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
   static_assert(!F16 || (EPI == EPI_STORE && BQ8 == B_BF16), "fp16 operands: plain store products");
 
-  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES];
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES + PJ_BYTES];
   float *sRed = (float *)(smem + LDS_BYTES);
+  char *pj_lds = smem + LDS_BYTES + RED_BYTES;
 
   // The wave index is uniform across the wave: readfirstlane tells the
   // compiler so, keeping every role test and loop counter that depends on it
@@ -596,6 +709,26 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
       if (s < nk) ART_ISSUE(s);
+    // Projection slice of this tile (SwiGLU epilogues): into LDS behind the
+    // first stages when it fits; the k-loop's waits and the barrier before
+    // the epilogue make it visible.
+    constexpr int PJ_NREG = EPI == EPI_SWIGLU_BWD ? 2 : 1;
+    constexpr int PJ_KC = EPI == EPI_SWIGLU_BWD ? BN : BN / 2;
+    int pj_col[PJ_NREG], pj_lim[PJ_NREG];
+    if constexpr (EPI == EPI_SWIGLU_BWD) {
+      pj_col[0] = nt * BN; pj_col[PJ_NREG - 1] = p.F + nt * BN;
+      pj_lim[0] = p.F; pj_lim[PJ_NREG - 1] = 2 * p.F;
+    } else {
+      pj_col[0] = nt * (BN / 2);
+      pj_lim[0] = p.F;
+    }
+    const bool pj_in_lds = EPI != EPI_STORE && p.pj_b &&
+                           PJ_NREG * p.pj_n * PJ_KC * 2 <= PJ_BYTES;
+    if constexpr (EPI != EPI_STORE && PJ_KC >= 128) {
+      if (pj_in_lds)
+        load_proj_slice<PJ_KC, PJ_NREG, NW>(pj_lds, p.pj_b + (int64_t)e * p.pj_es, p.pj_ld,
+                                            pj_col, pj_lim, p.pj_n, wave, lane);
+    }
 
     // Wait until stage ks has landed (at most min(STAGES-2, nk-1-ks) later
     // groups may still be in flight), then release the slot ks+STAGES-1 reuses.
@@ -858,6 +991,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
           *(U4 *)(p.h + (int64_t)m * F + f) = U4{lo.x, lo.y, hi.x, hi.y};
         }
       }
+      // fused LoRA down-projection of h: t2 partial of this column tile
+      if constexpr (EPI == EPI_SWIGLU_FWD) if (p.pj_b) {
+        epi_lora_proj<BN / 2, UPR2, UMASK2, 1, 0, BM, NW>(
+            stg, (PJ_KC >= 128 && pj_in_lds) ? pj_lds : nullptr, p.pj_b + (int64_t)e * p.pj_es,
+            p.pj_ld, pj_col, pj_lim, p.pj_n, 0, p.pj_part + (int64_t)nt * p.M * p.pj_n, p.M, m0,
+            m_end, wave, lane, [](int r) { return r; });
+      }
     } else {  // EPI_SWIGLU_BWD: acc = dh over columns f of this tile
       // Rows go in EPI2_NH groups (i = h*TMG .. h*TMG+TMG-1 of every wave):
       // each group's dg and du are staged side by side (two regions of
@@ -919,6 +1059,15 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
           const int m = m0 + row, f = nt * BN + ch * 8;
           if (m < m_end && f < F)
             *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + region * F + f) = load_chunk(region * RG + lr, ch);
+        }
+        // fused LoRA projection of dy1 = [dg | du]: g1 partial of this column
+        // tile (dg against P columns f, du against P columns F + f)
+        if constexpr (EPI == EPI_SWIGLU_BWD) if (p.pj_b) {
+          epi_lora_proj<BN, UPR, UMASK, 2, RG, RG, NW>(
+              stg, (PJ_KC >= 128 && pj_in_lds) ? pj_lds : nullptr, p.pj_b + (int64_t)e * p.pj_es,
+              p.pj_ld, pj_col, pj_lim, p.pj_n, p.pj_split,
+              p.pj_part + (int64_t)nt * p.M * p.pj_n, p.M, m0, m_end, wave, lane,
+              [&](int lr) { return (lr / WRG) * WTM + h * WRG + (lr % WRG); });
         }
         if (h + 1 < EPI2_NH) barrier_nofence();  // the next group reuses the regions
       }
@@ -1046,11 +1195,49 @@ static int launch_fp8(int fmt, const NTArgs &p, const int32_t *seg, int64_t M, h
   return launch_nt<256, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
 }
 
-static int tile_cfg(int dflt) {
-  const char *v = getenv("ART_MOE_GEMM_TILE");
+// Macro tile of one product: ART_MOE_GEMM_TILE_<which> (STORE, FC1 or BWD),
+// else ART_MOE_GEMM_TILE, else the default.
+static int tile_cfg(int dflt, const char *which) {
+  char name[64];
+  snprintf(name, sizeof(name), "ART_MOE_GEMM_TILE_%s", which);
+  const char *v = getenv(name);
+  if (!v || !*v) v = getenv("ART_MOE_GEMM_TILE");
   if (!v || !*v) return dflt;
   const int c = atoi(v);
   return (c >= 0 && c < kNumTileCfgs) ? c : dflt;
+}
+
+// Column width of macro tile config c (launch_big) and of the fp8 products.
+static int cfg_bn(int c) {
+  switch (c) {
+    case 0: case 2: case 4: case 9: case 10: case 12: case 17: return 128;
+    default: return 256;
+  }
+}
+
+// Output columns per column tile of the SwiGLU products: FC1 tiles cover BN/2
+// columns of h, the FC2 data gradient BN columns of dg (and of du).
+static int swiglu_tile_cols(int product, int32_t fmt) {
+  if (product == 0)
+    return (fmt == ART_MOE_B_BF16 ? cfg_bn(tile_cfg(kTileSwigluFwd, "FC1")) : 256) / 2;
+  return fmt == ART_MOE_B_BF16 ? cfg_bn(tile_cfg(kTileSwigluBwd, "BWD")) : 256;
+}
+
+// Sum of the projection partials in tile order: out[m][n] = bf16(sum_t
+// part[t][m][n]) for rows inside the segments, 0 past seg[E].  One thread per
+// 4 consecutive n.
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float *__restrict__ part, int nt,
+                                                        int64_t M, int N, const int32_t *seg,
+                                                        int E, bf16 *__restrict__ out,
+                                                        int64_t ldo) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= M * N) return;
+  const int64_t m = i / N;
+  const int n = (int)(i - m * N);
+  f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (!seg || m < seg[E])
+    for (int t = 0; t < nt; ++t) s += *(const f32x4 *)(part + (int64_t)t * M * N + i);
+  *(uint2 *)(out + m * ldo + n) = pack4(s[0], s[1], s[2], s[3]);
 }
 
 }  // namespace art
@@ -1058,6 +1245,47 @@ static int tile_cfg(int dflt) {
 using namespace art;
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int art_moe_lora_epilogue_parts(int32_t product, int32_t F, int32_t w_format) {
+  if (F <= 0 || (product != 0 && product != 1)) return 0;
+  const int cols = swiglu_tile_cols(product, w_format);
+  return (F + cols - 1) / cols;
+}
+
+extern "C" int art_moe_sum_parts(const float *part, int32_t n_parts, int64_t M, int32_t N,
+                                 const int32_t *seg, int32_t E, void *out, int64_t ldo,
+                                 void *stream) {
+  clear_error();
+  ART_REQUIRE(n_parts >= 1 && M >= 0 && N > 0 && N % 4 == 0,
+              "sum_parts: need n_parts >= 1, M >= 0, N %% 4 == 0 (n_parts=%d N=%d)", n_parts, N);
+  ART_REQUIRE(ldo >= N && ldo % 4 == 0, "sum_parts: need ldo >= N, ldo %% 4 == 0");
+  ART_REQUIRE(!seg || E >= 1, "sum_parts: seg needs E >= 1");
+  if (M == 0) return ART_MOE_OK;
+  ART_REQUIRE(part && out && aligned16(part) && ((uintptr_t)out & 7) == 0,
+              "sum_parts: null or misaligned buffer");
+  const int64_t threads = M * N / 4;
+  sum_parts_kernel<<<dim3((unsigned)((threads + 255) / 256)), 256, 0, as_stream(stream)>>>(
+      part, n_parts, M, N, seg, E, (bf16 *)out, ldo);
+  return check_launch("sum_parts");
+}
+
+// Projection arguments of the SwiGLU products (shared checks).
+static int set_projection(NTArgs &p, const void *pj_b, int64_t pj_es, int32_t pj_ld, int32_t pj_n,
+                          float *pj_part, int32_t pj_tiles, int product, int32_t fmt, int32_t F,
+                          int32_t width, const char *who) {
+  if (!pj_b) return ART_MOE_OK;
+  const int want = art_moe_lora_epilogue_parts(product, F, fmt);
+  ART_REQUIRE(pj_tiles == want, "%s: projection partials need %d column tiles, got %d "
+              "(art_moe_lora_epilogue_parts)", who, want, pj_tiles);
+  ART_REQUIRE(pj_n > 0 && pj_n % 16 == 0, "%s: projection width must be a multiple of 16 (%d)", who,
+              pj_n);
+  ART_REQUIRE(pj_ld >= width && pj_ld % 8 == 0 && pj_es >= (int64_t)pj_n * pj_ld,
+              "%s: projection operand rows must hold %d columns (ld %% 8 == 0)", who, width);
+  ART_REQUIRE(pj_part && aligned16(pj_b) && aligned16(pj_part), "%s: projection buffers must be "
+              "16-byte aligned", who);
+  p.pj_b = (const bf16 *)pj_b; p.pj_es = pj_es; p.pj_ld = pj_ld; p.pj_n = pj_n; p.pj_part = pj_part;
+  return ART_MOE_OK;
+}
 
 // Shared argument checks: operand rows are moved in 16-byte chunks and MFMA
 // steps are 16 wide, so base pointers are 16-byte aligned, leading dimensions
@@ -1160,7 +1388,7 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
   if (N <= 32) return launch_nt<128, 32, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n32");
   if (N <= 64) return launch_nt<128, 64, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n64");
   if (N <= 128) return launch_nt<128, 128, 2, 2, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n128");
-  return launch_big<EPI_STORE>(tile_cfg(kTileStore), p, seg, M, s, "grouped_gemm");
+  return launch_big<EPI_STORE>(tile_cfg(kTileStore, "STORE"), p, seg, M, s, "grouped_gemm");
 }
 
 extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
@@ -1168,7 +1396,8 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
                                   const void *tl, int64_t ldt, const void *l1,
                                   int32_t kt, const int32_t *seg, int32_t E, int64_t M, int32_t F,
                                   int32_t K, const float *row_prob, void *y1, void *h,
-                                  void *stream) {
+                                  const void *pj_b, int64_t pj_es, int32_t pj_ld, int32_t pj_n,
+                                  float *pj_part, int32_t pj_tiles, void *stream) {
   clear_error();
   int rc = check_common(a, lda, w1, K, seg, E, M, K, kt, tl, ldt, l1, kt, "fc1_swiglu");
   if (rc) return rc;
@@ -1187,9 +1416,12 @@ extern "C" int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_r
   p.l = kt ? (const bf16 *)l1 : nullptr; p.ldl = kt; p.l_es = (int64_t)2 * F * kt; p.kt = kt;
   p.E = E; p.N = 2 * F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;
   p.y1 = (bf16 *)y1; p.h = (bf16 *)h; p.M = M;
+  rc = set_projection(p, pj_b, pj_es, pj_ld, pj_n, pj_part, pj_tiles, 0, w1_format, F, F,
+                      "fc1_swiglu");
+  if (rc) return rc;
   if (w1_format != ART_MOE_B_BF16)
     return launch_fp8<EPI_SWIGLU_FWD>(w1_format, p, seg, M, as_stream(stream), "fc1_swiglu/fp8");
-  return launch_big<EPI_SWIGLU_FWD>(tile_cfg(kTileSwigluFwd), p, seg, M, as_stream(stream),
+  return launch_big<EPI_SWIGLU_FWD>(tile_cfg(kTileSwigluFwd, "FC1"), p, seg, M, as_stream(stream),
                                     "fc1_swiglu");
 }
 
@@ -1201,7 +1433,9 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
                                         const void *l2, int32_t kt, const int32_t *seg, int32_t E,
                                         int64_t M, int32_t F, int32_t K, const void *y1,
                                         const float *row_prob, void *dy1, float *dp_part,
-                                        void *stream) {
+                                        const void *pj_b, int64_t pj_es, int32_t pj_ld,
+                                        int32_t pj_n, int32_t pj_split, float *pj_part,
+                                        int32_t pj_tiles, void *stream) {
   clear_error();
   int rc = check_common(a, lda, w2t, K, seg, E, M, K, kt, tl, ldt, l2, kt, "fc2_dgrad_swiglu");
   if (rc) return rc;
@@ -1222,9 +1456,16 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
   p.l = kt ? (const bf16 *)l2 : nullptr; p.ldl = kt; p.l_es = (int64_t)F * kt; p.kt = kt;
   p.E = E; p.N = F; p.K = K; p.alpha = 1.0f; p.F = F; p.prob = row_prob;
   p.y1_in = (const bf16 *)y1; p.dy1 = (bf16 *)dy1; p.dp_part = dp_part; p.M = M;
+  rc = set_projection(p, pj_b, pj_es, pj_ld, pj_n, pj_part, pj_tiles, 1, w2_format, F, 2 * F,
+                      "fc2_dgrad_swiglu");
+  if (rc) return rc;
+  ART_REQUIRE(!pj_b || pj_split == 0 || (pj_split > 0 && pj_split < pj_n && pj_split % 16 == 0),
+              "fc2_dgrad_swiglu: pj_split must be 0 or a multiple of 16 below pj_n (%d, %d)",
+              pj_split, pj_n);
+  p.pj_split = pj_b ? pj_split : 0;
   if (w2_format != ART_MOE_B_BF16)
     return launch_fp8<EPI_SWIGLU_BWD>(w2_format, p, seg, M, as_stream(stream),
                                       "fc2_dgrad_swiglu/fp8");
-  return launch_big<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwd), p, seg, M, as_stream(stream),
+  return launch_big<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwd, "BWD"), p, seg, M, as_stream(stream),
                                     "fc2_dgrad_swiglu");
 }

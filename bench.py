@@ -40,7 +40,7 @@ NAMES = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
 GEMM_OPS = ("grouped_gemm", "fc1_swiglu", "fc2_dgrad_swiglu", "grouped_wgrad")
 HBM_OPS = ("router_topk", "router_replay", "dispatch_plan", "combine", "router_backward",
            "permute", "transpose_into", "segments_from_counts", "pack", "router_lora_apply",
-           "router_lora_grad", "quantize_rows_fp8")
+           "router_lora_grad", "quantize_rows_fp8", "sum_parts")
 
 
 class OpTimer:
@@ -252,7 +252,8 @@ def main():
 
     # dominant kernel: FC1 + LoRA K-extension + SwiGLU forward (one launch per step)
     m, h, f, r = cfg.M, cfg.H, cfg.F, cfg.r
-    fc1_flops = 2 * m * h * 2 * f + 2 * m * 2 * f * r
+    # base + LoRA K-extension + the fused down-projection h A_d of the epilogue
+    fc1_flops = 2 * m * h * 2 * f + 2 * m * 2 * f * r + 2 * m * f * r
     fc1_ms = tot_fc1["fc1_swiglu"] / max(cnt_fc1["fc1_swiglu"], 1)   # timed region
     fc1_tflops = fc1_flops / (fc1_ms * 1e-3) / 1e12
     gemm_ms = sum(tot[n] for n in GEMM_OPS) / args.steps
@@ -288,7 +289,7 @@ def main():
                                      "product (bf16 MFMA)") if cfg.fp8 else "bf16"),
                    "lora_grads": "fp32 main_grad accumulation" if cfg.router_r else "bf16 (param dtype)",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd)",
+        "roofline": {"bound": "mfma", "kernel": "fc1_swiglu (FC1 + LoRA K-extension + weighted SwiGLU fwd + fused h A_d partials)",
                      "achieved": round(fc1_tflops, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(fc1_tflops / peak, 4),
                      "traffic": measured_traffic(cfg.name),

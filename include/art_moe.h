@@ -226,14 +226,38 @@ int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a_rows,
  * W1 is bf16 (w1_format ART_MOE_B_BF16) or fp8 with per-row scales
  * w1_scale [E][2F] (ART_MOE_B_FP8_ROWSCALE, or ART_MOE_AB_FP8 with fp8 A
  * and a_scale as in art_moe_grouped_gemm).
+ * Fused LoRA down-projection (optional, pj_b != NULL): with pj_b [E][pj_n]
+ * [pj_ld] bf16 (the down adapter's A transposed, rank padded to pj_n, a
+ * multiple of 16), each column tile t of h writes the fp32 partial
+ *   pj_part[t][m][n] = sum_{f in tile t} h[m, f] * pj_b[e][n][f]
+ * for the rows of the segments (pj_part [pj_tiles][M][pj_n], pj_tiles =
+ * art_moe_lora_epilogue_parts(0, F, w1_format)); art_moe_sum_parts then
+ * gives t = h @ A_d per row, the input of the FC2 LoRA K-extension.
  * Replaces: MLPExpertsLinearFC1LoRA.forward (lora.py:1512-1529) followed by
- * weighted_bias_swiglu_impl (compile_workarounds.py:73-106). */
+ * weighted_bias_swiglu_impl (compile_workarounds.py:73-106), and the LoRA
+ * projection x @ A of the down adapter's forward (QuACK
+ * cute_grouped_lora_quack.py:337-373, the h @ A_d product). */
 int art_moe_fc1_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
                        const float *a_scale, const void *w1, const float *w1_scale, int32_t w1_format,
                        const void *tl, int64_t ldt,
                        const void *l1, int32_t kt, const int32_t *seg,
                        int32_t E, int64_t M, int32_t F, int32_t K,
-                       const float *row_prob, void *y1, void *h, void *stream);
+                       const float *row_prob, void *y1, void *h,
+                       const void *pj_b, int64_t pj_es, int32_t pj_ld, int32_t pj_n,
+                       float *pj_part, int32_t pj_tiles, void *stream);
+
+/* Number of column tiles (fp32 partial slices) the fused LoRA projection of
+ * art_moe_fc1_swiglu (product 0) or art_moe_fc2_dgrad_swiglu (product 1)
+ * writes for width F and weight format w_format, under the active tile
+ * configuration. */
+int art_moe_lora_epilogue_parts(int32_t product, int32_t F, int32_t w_format);
+
+/* out[m][n] = bf16(sum_{t < n_parts} part[t][m][n]) (part fp32 [n_parts][M]
+ * [N], summed in t order: deterministic) for rows m < seg[E] (all rows when
+ * seg is NULL), 0 for the rows past the segments.  N % 4 == 0, out rows of
+ * ldo bf16.  Completes the fused LoRA projections. */
+int art_moe_sum_parts(const float *part, int32_t n_parts, int64_t M, int32_t N,
+                      const int32_t *seg, int32_t E, void *out, int64_t ldo, void *stream);
 
 /* Number of fp32 partial vectors art_moe_fc2_dgrad_swiglu writes to dp_part. */
 int art_moe_dgrad_swiglu_parts(int32_t F);
@@ -251,15 +275,28 @@ int art_moe_dgrad_swiglu_parts(int32_t F);
  * with ART_MOE_AB_FP8, A is fp8 with a_scale per row and the per-k weight
  * scales must already be folded into A (art_moe_quantize_rows_fp8 with
  * col_scale); w2_scale is then an optional per-row (F) scale.
+ * Fused LoRA projection of dy1 (optional, pj_b != NULL): with pj_b
+ * [E][pj_n][pj_ld] bf16 (pj_ld >= 2F; the FC1 adapter's scaled B, e.g. the
+ * block-diagonal [[s_g B_g, 0], [0, s_u B_u]] rank-padded), column tile t
+ * writes pj_part[t][m][n] = sum_{f in tile t} (dy1[m, f] pj_b[e][n][f] +
+ * dy1[m, F + f] pj_b[e][n][F + f]); pj_tiles =
+ * art_moe_lora_epilogue_parts(1, F, w2_format); art_moe_sum_parts gives
+ * g = dy1 @ pj_b[e]^T, the FC1 LoRA data-gradient intermediate.  pj_split
+ * > 0 (a multiple of 16 below pj_n) declares pj_b block-diagonal: rows
+ * n < pj_split read columns < F only, rows n >= pj_split columns >= F only
+ * (the other blocks are taken as zero and never read); 0: a full operand.
  * Replaces: TE GroupedLinear dgrad of FC2 + QuACK LoRA dgrad
- * (cute_grouped_lora_quack.py:394-410) + weighted_swiglu_back. */
+ * (cute_grouped_lora_quack.py:394-410) + weighted_swiglu_back, and the
+ * dual adapter's grad_out @ B^T products (:522-546). */
 int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_t *a_rows,
                              const float *a_scale, const void *w2t, const float *w2_scale,
                              int32_t w2_format, const void *tl, int64_t ldt,
                              const void *l2, int32_t kt, const int32_t *seg,
                              int32_t E, int64_t M, int32_t F, int32_t K,
                              const void *y1, const float *row_prob, void *dy1,
-                             float *dp_part, void *stream);
+                             float *dp_part, const void *pj_b, int64_t pj_es,
+                             int32_t pj_ld, int32_t pj_n, int32_t pj_split,
+                             float *pj_part, int32_t pj_tiles, void *stream);
 
 #define ART_MOE_WGRAD_STORE 0
 #define ART_MOE_WGRAD_ACCUMULATE 1

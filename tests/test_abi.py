@@ -64,8 +64,14 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
     assert b"multiple of 16" in lib.art_moe_last_error()
     rc = lib.art_moe_fc1_swiglu(null, 64, null, null, null, null, 0, null, 0, null, 0, null, 4, 16,
-                                100, 64, null, null, null, null)
+                                100, 64, null, null, null, null, 0, 0, 0, null, 0, null)
     assert rc == _lib.ART_MOE_ERR_INVALID_ARG
+    # fused LoRA projection: partial count of the active tile configuration
+    assert lib.art_moe_lora_epilogue_parts(0, 768, _lib.B_BF16) == 6
+    assert lib.art_moe_lora_epilogue_parts(1, 768, _lib.B_BF16) == 3
+    assert lib.art_moe_lora_epilogue_parts(2, 768, _lib.B_BF16) == 0
+    rc = lib.art_moe_sum_parts(null, 0, 16, 16, null, 0, null, 16, null)
+    assert rc == _lib.ART_MOE_ERR_INVALID_ARG and b"n_parts >= 1" in lib.art_moe_last_error()
     # fp8 weights: K must be a multiple of 64 (checked before any pointer is used)
     buf = ctypes.create_string_buffer(4096 + 16)
     base = (ctypes.addressof(buf) + 15) // 16 * 16

@@ -353,3 +353,74 @@ def test_tile_config_partial_k(device, tile, k, monkeypatch):
     assert rel(y1, ref) < 1e-2
     gg, uu = y1.cpu().float().chunk(2, dim=1)
     assert rel(hh, torch.nn.functional.silu(gg) * uu * prob[:, None]) < 1e-2
+
+
+# ----------------------------------------------- LoRA projections in epilogues
+@pytest.mark.parametrize("e,m,f,h,rp,tile", [
+    (8, 1200, 512, 256, 16, None),      # default macro tile
+    (8, 1000, 576, 256, 32, None),      # F not a multiple of the 128-column tiles
+    (16, 3000, 768, 512, 48, "6"),      # another macro tile (4 x 2 waves)
+    (4, 300, 192, 128, 64, "0"),        # 128 x 128 tiles: 64 h columns per tile
+])
+def test_fc1_epilogue_projection(device, e, m, f, h, rp, tile, monkeypatch):
+    """t = h @ P^T from FC1's epilogue (fp32 partials per column tile, summed
+    in order) equals the fp32 product of the kernel's own bf16 h, per expert
+    segment; rows past the segments are 0."""
+    if tile is not None:
+        monkeypatch.setenv("ART_MOE_GEMM_TILE_FC1", tile)
+    ops = _ops()
+    print(f"fc1 projection e={e} m={m} f={f} rp={rp} tile={tile}", flush=True)
+    g = torch.Generator().manual_seed(f + rp)
+    counts = _counts(e, m - 37, seed=f)          # 37 rows past the last segment
+    seg = ops.segments_from_counts(counts, e, device)
+    x = torch.randn(m, h, generator=g).to(torch.bfloat16).to(device)
+    w1 = (torch.randn(e, 2 * f, h, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    prob = torch.rand(m, generator=g).to(device)
+    proj = (torch.randn(e, rp, f, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    y1, hh, part = ops.fc1_swiglu(x, w1, seg, e, prob, m=m, proj=proj)
+    t = ops.sum_parts(part, seg)
+    y1b, hb = ops.fc1_swiglu(x, w1, seg, e, prob, m=m)
+    torch.cuda.synchronize()
+    cut = sum(counts)
+    assert torch.equal(hh[:cut], hb[:cut]) and torch.equal(y1[:cut], y1b[:cut])
+    ref = _ref_grouped(hh[:cut].float().cpu(), proj.cpu(), counts)
+    assert rel(t[:cut], ref) < 1e-2
+    assert torch.count_nonzero(t[cut:]) == 0
+
+
+@pytest.mark.parametrize("e,m,f,h,rp,tile,split", [
+    (8, 1000, 512, 256, 32, None, 0),
+    (8, 1000, 512, 256, 32, None, 16),  # block-diagonal operand (the dual adapter)
+    (8, 900, 200, 256, 16, None, 0),    # F not a multiple of the column tiles
+    (8, 700, 384, 256, 128, None, 64),  # slice too large for LDS: global reads
+    (16, 3000, 768, 512, 64, "3", 32),  # 128 x 256, 3 stages
+])
+def test_fc2_dgrad_epilogue_projection(device, e, m, f, h, rp, tile, split, monkeypatch):
+    """g = dy1 @ P^T from the FC2-dgrad epilogue (P [E, rp, 2F] over the dg
+    and du halves) equals the fp32 product of the kernel's own bf16 dy1; with
+    a split the off-diagonal blocks of P are ignored (filled with noise here)."""
+    if tile is not None:
+        monkeypatch.setenv("ART_MOE_GEMM_TILE_BWD", tile)
+    ops = _ops()
+    print(f"fc2 dgrad projection e={e} m={m} f={f} rp={rp} tile={tile} split={split}", flush=True)
+    g = torch.Generator().manual_seed(f * 3 + rp)
+    counts = _counts(e, m - 21, seed=f + 1)
+    seg = ops.segments_from_counts(counts, e, device)
+    dy = torch.randn(m, h, generator=g).to(torch.bfloat16).to(device)
+    w2t = (torch.randn(e, f, h, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    y1 = torch.randn(m, 2 * f, generator=g).to(torch.bfloat16).to(device)
+    prob = torch.rand(m, generator=g).to(device)
+    proj = (torch.randn(e, rp, 2 * f, generator=g) * 0.05).to(torch.bfloat16)
+    dy1, dp, part = ops.fc2_dgrad_swiglu(dy, w2t, seg, e, y1, prob, m=m, proj=proj.to(device),
+                                         proj_split=split)
+    gp = ops.sum_parts(part, seg)
+    dy1b, dpb = ops.fc2_dgrad_swiglu(dy, w2t, seg, e, y1, prob, m=m)
+    torch.cuda.synchronize()
+    cut = sum(counts)
+    assert torch.equal(dy1[:cut], dy1b[:cut]) and torch.equal(dp[:, :cut], dpb[:, :cut])
+    if split:
+        proj[:, :split, f:] = 0
+        proj[:, split:, :f] = 0
+    ref = _ref_grouped(dy1[:cut].float().cpu(), proj, counts)
+    assert rel(gp[:cut], ref) < 1e-2
+    assert torch.count_nonzero(gp[cut:]) == 0
