@@ -33,6 +33,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace art {
@@ -345,8 +347,20 @@ __device__ __forceinline__ bf16x8 scale_frag(bf16x8 v, float s) {
 // fp16 MFMA; otherwise bfloat16).
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// Calls f(std::integral_constant<int, v>) for a run-time 0 <= v <= N, so that
+// f is compiled once per value.
+template <int N, typename F>
+__device__ __forceinline__ void dispatch_count(int v, F &f) {
+  if constexpr (N == 0) {
+    f(std::integral_constant<int, 0>{});
+  } else {
+    if (v >= N) f(std::integral_constant<int, N>{});
+    else dispatch_count<N - 1>(v, f);
+  }
+}
+
 // Row blocks i >= tmv hold no valid row of the tile: their MFMAs are skipped
-// (tmv is wave-uniform, so each test is one scalar branch).
+// (callers pass tmv as a compile-time count: see dispatch_count).
 template <int TM, int TN, bool F16 = false>
 __device__ __forceinline__ void mma_step(f32x16 (&acc)[TM][TN], const bf16x8 (&af)[TM],
                                          const bf16x8 (&bfv)[TN], int tmv = TM) {
@@ -384,7 +398,8 @@ constexpr int epi2_groups(int tm, int bm, int bn, int lds_bytes) {
 }
 
 // LoRA projection of an epilogue tile staged in LDS (bf16 rows of 8-byte
-// units, unit u of staging row r at stg[r * UPR + (u ^ (r & UMASK))]):
+// units, unit u of staging row r at stg[r * UPR + (u ^ (r & UMASK))]; the 32
+// columns of k step kk start at unit kk * UB):
 //   part[t][m0 + row_of(r)][n] = sum_g sum_{c < KC} T_g[r][c] * P[n][pcol_g + c]
 // over NREG staged regions g (region g's rows start at staging row
 // g * REG_ROWS; its P columns at pcol[g]), for the staging rows r < NR and
@@ -397,7 +412,8 @@ constexpr int epi2_groups(int tm, int bm, int bn, int lds_bytes) {
 // P comes from the tile's slice in LDS (pj_lds: [NREG][NQ][KC] with the 16-
 // byte chunk c of row n at c ^ (n & 15), see load_proj_slice) or, when that
 // is null, straight from global memory.
-template <int KC, int UPR, int UMASK, int NREG, int REG_ROWS, int NR, int NW, typename RowOf>
+template <int KC, int UPR, int UMASK, int UB, int NREG, int REG_ROWS, int NR, int NW,
+          typename RowOf>
 __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_lds, const bf16 *P,
                                               int ldp, const int (&pcol)[NREG],
                                               const int (&plim)[NREG], int NQ, int split,
@@ -427,7 +443,7 @@ __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_l
         for (int j = 0; j < 2; ++j) {
           if (k0 + j >= KS) continue;
           const int kk = k0 + j;
-          const int u = kk * 8 + 2 * g4;               // first 8-byte unit of the lane's k run
+          const int u = kk * UB + 2 * g4;              // first 8-byte unit of the lane's k run
           const uint2 lo = stg[r * UPR + (u ^ (r & UMASK))];
           const uint2 hi = stg[r * UPR + ((u + 1) ^ (r & UMASK))];
           a4[j] = U4{lo.x, lo.y, hi.x, hi.y};
@@ -594,7 +610,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // multiplied.  Rows past m_end are never stored, and each output row
     // depends on its own A row only, so what those LDS rows hold is moot.
     const int vrows = (p.sched & 4) ? m_end - m0 : BM;
-    const int tmv = min(max((vrows - wm * WTM + 31) >> 5, 0), TM);
+    const int tmv_rt = min(max((vrows - wm * WTM + 31) >> 5, 0), TM);
     const int a_blocks = (STAGES == 2 && !A8) ? (vrows + RPB - 1) / RPB : (1 << 30);
 
     // Source rows of this lane's DMA slots (clamped into the segment / N), as
@@ -754,6 +770,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     if (!late_issue && (ks) + STAGES - 1 < nk) ART_ISSUE((ks) + STAGES - 1);                  \
   } while (0)
 
+    // The k-loop below is compiled once per count tmv = 0 .. TM of valid row
+    // blocks of this wave (tmv_rt picks one per tile), so that the skipped
+    // blocks cost no branch at each MFMA or fragment read.
+    auto k_loop = [&](auto tmv_c) __attribute__((always_inline)) {
+    constexpr int tmv = decltype(tmv_c)::value;
     // Full k-tiles of the base product: branch-free, fragments of step kk+1
     // are read while step kk multiplies.  (A separate loop keeps the
     // accumulators in one register assignment across iterations.)
@@ -858,6 +879,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         mma_step<TM, TN, F16>(acc, af, bfv, tmv);
       }
     }
+    };
+    dispatch_count<TM>(tmv_rt, k_loop);
 #undef ART_STAGE_IN
 #undef ART_STAGE_IN_STAGGERED
 #undef ART_ISSUE
@@ -933,67 +956,59 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       }
     } else if (EPI == EPI_SWIGLU_FWD) {
       const int F = p.F;
-      // pass 1: y1 (gate and up, rounded to bf16) in logical column order
-      float hv[TM][TN / 2][16];
+      // pass 1: gate and up rounded to bf16, staged per 64-column physical
+      // block as [32 gate | 32 up] (units ug .. ug+7 gate, ug+8 .. ug+15 up)
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = wm * WTM + i * 32 + lrow;
-        const int m = m0 + row;
-        const float pr = p.prob[m < m_end ? m : m_end - 1];
 #pragma unroll
         for (int jp = 0; jp < TN / 2; ++jp)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            float gq[4], uq[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              gq[v] = (float)(bf16)acc[i][2 * jp][4 * q + v];
-              uq[v] = (float)(bf16)acc[i][2 * jp + 1][4 * q + v];
-              hv[i][jp][4 * q + v] = silu_f(gq[v]) * uq[v] * pr;
-            }
             const int ug = (wn * WTN + 2 * jp * 32) / 4 + 2 * q + lk;
-            stage_unit(row, ug, pack4(gq[0], gq[1], gq[2], gq[3]));
-            stage_unit(row, ug + 8, pack4(uq[0], uq[1], uq[2], uq[3]));
+            stage_unit(row, ug, pack4(acc[i][2 * jp][4 * q], acc[i][2 * jp][4 * q + 1],
+                                      acc[i][2 * jp][4 * q + 2], acc[i][2 * jp][4 * q + 3]));
+            stage_unit(row, ug + 8,
+                       pack4(acc[i][2 * jp + 1][4 * q], acc[i][2 * jp + 1][4 * q + 1],
+                             acc[i][2 * jp + 1][4 * q + 2], acc[i][2 * jp + 1][4 * q + 3]));
           }
       }
       barrier_nofence();
-      for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
-        const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
-        const int blk = ch >> 2;  // 32-column logical block
-        const int f = nt * (BN / 2) + (blk >> 1) * 32 + (ch & 3) * 8;
-        const int m = m0 + row;
-        if (m < m_end && f < F)
-          *(U4 *)(p.y1 + (int64_t)m * (2 * F) + ((blk & 1) ? F : 0) + f) = load_chunk(row, ch);
-      }
-      barrier_nofence();
-      // pass 2: h = silu(g) * u * p, tile-local columns 0 .. BN/2-1 (staging rows of BN/2)
-      constexpr int UPR2 = BN / 8;
-      constexpr int UMASK2 = (UPR2 >= 32) ? 31 : (UPR2 - 1);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int jp = 0; jp < TN / 2; ++jp)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int row = wm * WTM + i * 32 + lrow;
-            const int unit = ((wn * TN) / 2 + jp) * 8 + 2 * q + lk;
-            stg[row * UPR2 + (unit ^ (row & UMASK2))] =
-                pack4(hv[i][jp][4 * q], hv[i][jp][4 * q + 1], hv[i][jp][4 * q + 2], hv[i][jp][4 * q + 3]);
-          }
-      barrier_nofence();
+      // pass 2, per (row, 8 h columns): y1's gate and up chunks out, then
+      // h = silu(g) * u * p from the same bf16 values, out and back into the
+      // gate chunk's units (the LoRA projection below reads h there; columns
+      // past F and rows past the segment hold zeros)
       for (int idx = tid; idx < BM * (BN / 16); idx += NT) {
         const int row = idx / (BN / 16), ch = idx - row * (BN / 16);
+        const int gch = (ch >> 2) * 8 + (ch & 3);        // gate chunk; up chunk gch + 4
+        const U4 g8 = load_chunk(row, gch), u8 = load_chunk(row, gch + 4);
         const int f = nt * (BN / 2) + ch * 8;
         const int m = m0 + row;
-        if (m < m_end && f < F) {
-          const uint2 lo = stg[row * UPR2 + ((2 * ch) ^ (row & UMASK2))];
-          const uint2 hi = stg[row * UPR2 + ((2 * ch + 1) ^ (row & UMASK2))];
-          *(U4 *)(p.h + (int64_t)m * F + f) = U4{lo.x, lo.y, hi.x, hi.y};
+        const bool ok = m < m_end && f < F;
+        U4 h8 = U4{0u, 0u, 0u, 0u};
+        if (ok) {
+          bf16 *y = p.y1 + (int64_t)m * (2 * F) + f;
+          *(U4 *)y = g8;
+          *(U4 *)(y + F) = u8;
+          const float pr = p.prob[m];
+          const uint32_t gw[4] = {g8.x, g8.y, g8.z, g8.w}, uw[4] = {u8.x, u8.y, u8.z, u8.w};
+          uint32_t hw[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float g0 = __uint_as_float(gw[w] << 16), g1 = __uint_as_float(gw[w] & 0xffff0000u);
+            const float u0 = __uint_as_float(uw[w] << 16), u1 = __uint_as_float(uw[w] & 0xffff0000u);
+            hw[w] = pack2(silu_f(g0) * u0 * pr, silu_f(g1) * u1 * pr);
+          }
+          h8 = U4{hw[0], hw[1], hw[2], hw[3]};
+          *(U4 *)(p.h + (int64_t)m * F + f) = h8;
         }
+        stage_unit(row, 2 * gch, uint2{h8.x, h8.y});
+        stage_unit(row, 2 * gch + 1, uint2{h8.z, h8.w});
       }
       // fused LoRA down-projection of h: t2 partial of this column tile
       if constexpr (EPI == EPI_SWIGLU_FWD) if (p.pj_b) {
-        epi_lora_proj<BN / 2, UPR2, UMASK2, 1, 0, BM, NW>(
+        barrier_nofence();
+        epi_lora_proj<BN / 2, UPR, UMASK, 16, 1, 0, BM, NW>(
             stg, (PJ_KC >= 128 && pj_in_lds) ? pj_lds : nullptr, p.pj_b + (int64_t)e * p.pj_es,
             p.pj_ld, pj_col, pj_lim, p.pj_n, 0, p.pj_part + (int64_t)nt * p.M * p.pj_n, p.M, m0,
             m_end, wave, lane, [](int r) { return r; });
@@ -1063,7 +1078,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         // fused LoRA projection of dy1 = [dg | du]: g1 partial of this column
         // tile (dg against P columns f, du against P columns F + f)
         if constexpr (EPI == EPI_SWIGLU_BWD) if (p.pj_b) {
-          epi_lora_proj<BN, UPR, UMASK, 2, RG, RG, NW>(
+          epi_lora_proj<BN, UPR, UMASK, 8, 2, RG, RG, NW>(
               stg, (PJ_KC >= 128 && pj_in_lds) ? pj_lds : nullptr, p.pj_b + (int64_t)e * p.pj_es,
               p.pj_ld, pj_col, pj_lim, p.pj_n, p.pj_split,
               p.pj_part + (int64_t)nt * p.M * p.pj_n, p.M, m0, m_end, wave, lane,
