@@ -148,6 +148,57 @@ def test_layer_fp8_weights_c4_widths(device, act_fp8):
     assert all(v < tol for v in errs.values()), errs
 
 
+def test_layer_fp8_c4_full_size_token_subset(device):
+    """Full C4 (E=128, T=16384, H=4096, F=1536, r=32) with fp8 e4m3fn weights
+    (W8A16) on the GPU; dy on 32 tokens.  Counts equal the histogram of the
+    selection, dx is zero off the subset, and the oracle on the subset (on the
+    dequantised weights, replaying the GPU's selection) matches y, dx and the
+    LoRA gradients to the bf16 bar."""
+    from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
+    from art_amd.quant import dequantize_fp8_rows, quantize_fp8_rows
+    from art_amd.workloads import CONFIGS, make_inputs
+    print("layer C4 full size fp8", flush=True)
+    cfg = CONFIGS["C4"]
+    inp = make_inputs(cfg, "cpu", seed=0)
+    gen = torch.Generator().manual_seed(13)
+    subset = torch.randperm(cfg.T, generator=gen)[:32].sort().values
+    dy = torch.zeros_like(inp.dy)
+    dy[subset] = inp.dy[subset]
+    q1, s1 = quantize_fp8_rows(inp.w1.to(device))
+    q2, s2 = quantize_fp8_rows(inp.w2.to(device))
+    base = FrozenExperts.build_fp8(inp.w_r.to(device), q1, s1, q2, s2)
+    names = ("a_g", "b_g", "a_u", "b_u", "a_d", "b_d")
+    lora = {n: inp.lora[n].to(device).requires_grad_() for n in names}
+    x = inp.x.to(device).requires_grad_()
+    s = cfg.scale
+    y, idx, counts, status = moe_lora_layer(x, base, *(lora[n] for n in names), k=cfg.k,
+                                            scales=(s, s, s))
+    y.backward(dy.to(device))
+    torch.cuda.synchronize()
+    idx, counts = idx.cpu(), counts.cpu()
+    assert int(status.item()) == 0 and int(counts.sum()) == cfg.T * cfg.k
+    assert counts.tolist() == np.bincount(idx.numpy().reshape(-1), minlength=cfg.E).tolist()
+    dx = x.grad.cpu()
+    outside = torch.ones(cfg.T, dtype=torch.bool)
+    outside[subset] = False
+    assert torch.count_nonzero(dx[outside]) == 0
+    w1d, w2d = dequantize_fp8_rows(q1, s1).cpu(), dequantize_fp8_rows(q2, s2).cpu()
+    del base, q1, q2
+    xo = inp.x[subset].float().requires_grad_()
+    leaves = {n: inp.lora[n].float().requires_grad_() for n in names}
+    p = OL.LayerParams(w_r=inp.w_r, w1=w1d, w2=w2d, scale_g=s, scale_u=s, scale_d=s, **leaves)
+    yo, _ = OL.moe_lora_layer(xo, p, cfg.k, target=idx[subset].long())
+    yo.backward(dy[subset].float())
+
+    def rel(a, b):
+        return ((a.double() - b.double()).norm() / b.double().norm()).item()
+    errs = {"y": rel(y.detach().cpu()[subset], yo.detach()), "dx": rel(dx[subset], xo.grad)}
+    for n in names:
+        errs["d" + n] = rel(lora[n].grad.cpu(), leaves[n].grad)
+    print("  rel errs", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert all(v < 2e-2 for v in errs.values()), errs
+
+
 # ----------------------------------------------------------------- W8A8
 # fp8 activations x fp8 weights on the f8f6f4 MFMA.  The quantiser must equal
 # torch's float8_e4m3fn conversion (round to nearest even) byte for byte; the

@@ -167,6 +167,41 @@ def test_layer_c1_full_size_token_subset(device):
     _compare(got_sub, ref, ["y", "dx"] + ["d" + n for n in NAMES])
 
 
+def _token_subset(T, n, seed):
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randperm(T, generator=gen)[:n].sort().values
+
+
+def test_layer_c2_full_size_replay_token_subset(device):
+    """Full C2 (T=8192, Zipf replay: empty experts, ragged segments, Dirichlet
+    gate weights) on the GPU; dy on 48 tokens.  The replayed indices equal the
+    targets bit for bit, the counts their histogram, dx and dlogits are zero off
+    the subset, and the oracle on the subset matches y, dx, dlogits and the
+    LoRA gradients."""
+    from art_amd.workloads import CONFIGS, make_inputs
+    print("layer C2 full size replay", flush=True)
+    cfg = CONFIGS["C2"]
+    inp = make_inputs(cfg, "cpu", seed=0)
+    subset = _token_subset(cfg.T, 48, 11)
+    dy = torch.zeros_like(inp.dy)
+    dy[subset] = inp.dy[subset]
+    got = _gpu_layer(inp, device, use_logits=True, use_target=True, dy=dy)
+    assert got["status"] == 0
+    assert torch.equal(got["idx"].long(), inp.target.long())
+    hist = np.bincount(inp.target.numpy().reshape(-1), minlength=cfg.E)
+    assert got["counts"].tolist() == hist.tolist() and (hist == 0).any()
+    outside = torch.ones(cfg.T, dtype=torch.bool)
+    outside[subset] = False
+    assert torch.count_nonzero(got["dx"][outside]) == 0
+    assert torch.count_nonzero(got["dlogits"][outside]) == 0
+    ref = _oracle_layer(inp, tokens=subset, logits_given=True, target=inp.target[subset].long(),
+                        dy=dy)
+    got_sub = dict(got)
+    for key in ("y", "dx", "dlogits"):
+        got_sub[key] = got[key][subset]
+    _compare(got_sub, ref, ["y", "dx", "dlogits"] + ["d" + n for n in NAMES])
+
+
 def _gpu_layer_router_lora(inp, device, *, fuse=False, main_grads=None, tokens_dy=None):
     from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
     cfg = inp.cfg
@@ -213,6 +248,43 @@ def test_layer_c3_router_lora(device):
     y.backward(inp.dy.float())
     ref = {"y": y.detach(), "dx": x.grad, **{"d" + n: leaves[n].grad for n in names}}
     _compare(got, ref, ["y", "dx"] + ["d" + n for n in names])
+
+
+def test_layer_c3_full_size_token_subset(device):
+    """Full C3 (T=32768, r=64, router LoRA rank 64, gradients landed in fp32
+    main_grad) on the GPU; dy on 32 tokens.  Counts equal the histogram of the
+    selection, dx is zero off the subset, and the oracle on the subset (replaying
+    the GPU's selection) matches y, dx and all eight LoRA gradients, read from
+    main_grad."""
+    from art_amd.workloads import CONFIGS, make_inputs
+    print("layer C3 full size", flush=True)
+    cfg = CONFIGS["C3"]
+    inp = make_inputs(cfg, "cpu", seed=0)
+    subset = _token_subset(cfg.T, 32, 12)
+    dy = torch.zeros_like(inp.dy)
+    dy[subset] = inp.dy[subset]
+    names = NAMES + ("a_r", "b_r")
+    mg = {n: torch.zeros(inp.lora[n].shape, dtype=torch.float32, device=device) for n in names}
+    got = _gpu_layer_router_lora(inp, device, fuse=True, main_grads=mg, tokens_dy=dy)
+    counts = got["counts"]
+    assert int(counts.sum()) == cfg.T * cfg.k
+    assert counts.tolist() == np.bincount(got["idx"].numpy().reshape(-1), minlength=cfg.E).tolist()
+    outside = torch.ones(cfg.T, dtype=torch.bool)
+    outside[subset] = False
+    assert torch.count_nonzero(got["dx"][outside]) == 0
+    for n in names:
+        assert got["d" + n] is None and got["added_" + n], n
+    sr = cfg.alpha / cfg.router_r
+    x = inp.x[subset].float().requires_grad_()
+    leaves = {n: inp.lora[n].float().requires_grad_() for n in names}
+    p = OL.LayerParams(w_r=inp.w_r, w1=inp.w1, w2=inp.w2, scale_g=cfg.scale, scale_u=cfg.scale,
+                       scale_d=cfg.scale, scale_r=sr, **leaves)
+    y, _ = OL.moe_lora_layer(x, p, cfg.k, target=got["idx"][subset].long())
+    y.backward(dy[subset].float())
+    ref = {"y": y.detach(), "dx": x.grad, **{"d" + n: leaves[n].grad for n in names}}
+    got_sub = {"y": got["y"][subset], "dx": got["dx"][subset],
+               **{"d" + n: mg[n].cpu() for n in names}}
+    _compare(got_sub, ref, ["y", "dx"] + ["d" + n for n in names])
 
 
 @pytest.mark.parametrize("cfg_name", ["C3", "C0"])
