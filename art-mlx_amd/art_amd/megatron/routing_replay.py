@@ -50,6 +50,7 @@ from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Any, Callable
 
+import numpy as np
 import torch
 
 logger = logging.getLogger(__name__)
@@ -169,7 +170,10 @@ class RouterCallRoute:
     """Captured top-k ids of one router call: ``expert_indices`` int32
     [tokens, k] (every slot valid: ``expert_mask`` all true), optional
     ``expert_probs``; ``sample_index`` / ``micro_slot`` say which micro it
-    belongs to (neither: the legacy call-order layout)."""
+    belongs to (neither: the legacy call-order layout).  ``expert_indices``
+    may live on a GPU (a view of a step's device route table, see
+    ``MoeRoutingReplayBundle.from_dir(device=...)``): its id range is then
+    checked where it was staged, not here."""
     expert_indices: torch.Tensor
     expert_mask: torch.Tensor
     num_experts: int
@@ -179,7 +183,13 @@ class RouterCallRoute:
     rank_token_counts: tuple[int, ...] | None = None
 
     def __post_init__(self) -> None:
-        self.expert_indices = _host(self.expert_indices, torch.int32, "expert_indices")
+        on_device = isinstance(self.expert_indices, torch.Tensor) and \
+            self.expert_indices.device.type != "cpu"
+        if on_device:
+            if self.expert_indices.dtype != torch.int32 or not self.expert_indices.is_contiguous():
+                raise RuntimeError("device expert_indices must be contiguous int32")
+        else:
+            self.expert_indices = _host(self.expert_indices, torch.int32, "expert_indices")
         self.expert_mask = _host(self.expert_mask, torch.bool, "expert_mask")
         if self.expert_probs is not None:
             self.expert_probs = _host(self.expert_probs, torch.float32, "expert_probs")
@@ -195,8 +205,9 @@ class RouterCallRoute:
         self.num_experts = int(self.num_experts)
         if self.num_experts <= 0:
             raise RuntimeError(f"num_experts must be positive, got {self.num_experts}")
-        if self.expert_indices.numel() and (int(self.expert_indices.min()) < 0 or
-                                            int(self.expert_indices.max()) >= self.num_experts):
+        if not on_device and self.expert_indices.numel() and (
+                int(self.expert_indices.min()) < 0 or
+                int(self.expert_indices.max()) >= self.num_experts):
             raise RuntimeError(f"expert_indices hold ids outside [0, {self.num_experts})")
         if self.sample_index is not None:
             self.sample_index = int(self.sample_index)
@@ -320,7 +331,7 @@ class MoeRoutingReplayBundle:
                 calls: dict[str, Any] = {}
                 for ci in sorted(step.routers[rk].calls):
                     route = step.routers[rk].calls[ci]
-                    tensors[_tensor_key(rk, ci, "expert_indices")] = route.expert_indices
+                    tensors[_tensor_key(rk, ci, "expert_indices")] = route.expert_indices.cpu()
                     tensors[_tensor_key(rk, ci, "expert_mask")] = route.expert_mask
                     if route.expert_probs is not None:
                         tensors[_tensor_key(rk, ci, "expert_probs")] = route.expert_probs
@@ -342,8 +353,17 @@ class MoeRoutingReplayBundle:
                                             encoding="utf-8")
 
     @classmethod
-    def from_dir(cls, bundle_dir: str | Path) -> "MoeRoutingReplayBundle":
+    def from_dir(cls, bundle_dir: str | Path, *,
+                 device: torch.device | str | None = None) -> "MoeRoutingReplayBundle":
+        """Load a bundle.  With a GPU ``device``, each step's expert ids go
+        from the file straight into one device route table per step (all
+        routers and calls back to back: read into pinned memory, range-checked
+        there, one host-to-device copy); masks, probabilities and token uids
+        stay host metadata."""
         from safetensors.torch import load_file
+        dev = torch.device(device) if device is not None else None
+        if dev is not None and dev.type == "cpu":
+            dev = None
         base = Path(bundle_dir)
         mpath = base / "manifest.json"
         if not mpath.exists():
@@ -356,7 +376,10 @@ class MoeRoutingReplayBundle:
         for si, sinfo in manifest["steps"].items():
             # clone: the loaded tensors may map the file, which must not stay
             # open (shared-filesystem cleanup) while a long-lived rank holds them
-            raw = {k: v.clone() for k, v in load_file(str(base / sinfo["file"])).items()}
+            if dev is None:
+                raw = {k: v.clone() for k, v in load_file(str(base / sinfo["file"])).items()}
+            else:
+                raw = _load_step_to_device(base / sinfo["file"], sinfo["routers"], dev)
             if GLOBAL_TOKEN_UIDS_KEY not in raw:
                 raise RuntimeError(f"{sinfo['file']} lacks '{GLOBAL_TOKEN_UIDS_KEY}'")
             routers: dict[str, StepRouterRoutes] = {}
@@ -380,6 +403,67 @@ class MoeRoutingReplayBundle:
                    num_steps=int(manifest["num_steps"]), max_topk=int(manifest["max_topk"]),
                    router_keys=list(manifest["router_keys"]), steps=steps,
                    format_version=manifest["format_version"])
+
+
+_SAFETENSORS_INT = {"I8": np.int8, "I16": np.int16, "I32": np.int32, "I64": np.int64,
+                    "U8": np.uint8, "U16": np.uint16, "U32": np.uint32, "U64": np.uint64}
+
+
+def _load_step_to_device(path: Path, routers: Mapping[str, Any],
+                         dev: torch.device) -> dict[str, torch.Tensor]:
+    """One step file: every ``expert_indices`` tensor read from the file into
+    one pinned int32 buffer (in router, call order), its ids checked against
+    the call's ``num_experts``, then one copy into a device table whose views
+    are returned; every other tensor is loaded on the host.  The file layout
+    is the safetensors one: an 8-byte little-endian header length, a JSON
+    header of {name: {dtype, shape, data_offsets}}, then the data."""
+    from safetensors import safe_open
+    with open(path, "rb") as fh:
+        hlen = int.from_bytes(fh.read(8), "little")
+        header = json.loads(fh.read(hlen))
+        data0 = 8 + hlen
+        ids = []
+        for rk in sorted(routers):
+            for ci in sorted(routers[rk], key=int):
+                name = _tensor_key(rk, int(ci), "expert_indices")
+                if name not in header:
+                    raise RuntimeError(f"{path.name} lacks ['{name}']")
+                info = header[name]
+                if info["dtype"] not in _SAFETENSORS_INT or len(info["shape"]) != 2:
+                    raise RuntimeError(f"{path.name}: {name} must be a 2-D integer tensor, got "
+                                       f"{info['dtype']} {info['shape']}")
+                ids.append((name, info, int(routers[rk][ci]["num_experts"])))
+        total = sum(int(np.prod(i["shape"])) for _, i, _ in ids)
+        pinned = torch.empty(total, dtype=torch.int32, pin_memory=True)
+        host = pinned.numpy()
+        views: list[tuple[str, int, tuple[int, int]]] = []
+        at = 0
+        for name, info, n_exp in ids:
+            b, e = (int(x) for x in info["data_offsets"])
+            shape = tuple(int(x) for x in info["shape"])
+            n = shape[0] * shape[1]
+            fh.seek(data0 + b)
+            dt = np.dtype(_SAFETENSORS_INT[info["dtype"]]).newbyteorder("<")
+            if e - b != n * dt.itemsize:
+                raise RuntimeError(f"{path.name}: {name} byte range does not match its shape")
+            if dt == np.dtype("<i4"):
+                fh.readinto(memoryview(host[at:at + n]).cast("B"))
+            else:
+                host[at:at + n] = np.frombuffer(fh.read(e - b), dtype=dt)
+            part = host[at:at + n]
+            if n and (int(part.min()) < 0 or int(part.max()) >= n_exp):
+                raise RuntimeError(f"expert_indices hold ids outside [0, {n_exp})")
+            views.append((name, at, shape))
+            at += n
+    table = torch.empty(total, dtype=torch.int32, device=dev)
+    table.copy_(pinned, non_blocking=True)
+    torch.cuda.current_stream(dev).synchronize()     # the pinned buffer is released below
+    raw = {name: table[a:a + sh[0] * sh[1]].view(sh) for name, a, sh in views}
+    with safe_open(str(path), framework="pt") as f:
+        for name in f.keys():
+            if name not in raw:
+                raw[name] = f.get_tensor(name).clone()
+    return raw
 
 
 # ---------------------------------------------------------- synthetic routes
@@ -1056,11 +1140,14 @@ class MoeRoutingReplayController:
                 if bool((rows >= route.num_global_tokens).any()):
                     raise RuntimeError(f"{where}: a token row is past the route's "
                                        f"{route.num_global_tokens} rows")
-                target = route.expert_indices.index_select(0, rows.clamp_min(0)).long()
+                src = route.expert_indices
+                target = src.index_select(0, rows.clamp_min(0).to(src.device)).long()
                 if neg.numel():
-                    target[neg] = self._synthetic(ci, neg, route.num_experts, route.max_topk).long()
-                self._micro.targets[(name, rk)] = self._upload(target) if dev.type == "cuda" \
-                    else target
+                    target[neg.to(src.device)] = self._synthetic(
+                        ci, neg, route.num_experts, route.max_topk).long().to(src.device)
+                if dev.type == "cuda" and target.device.type == "cpu":
+                    target = self._upload(target)
+                self._micro.targets[(name, rk)] = target
         if dev.type == "cuda" and self._micro.targets:
             ready = torch.cuda.Event()
             ready.record(self._side_stream())
@@ -1092,8 +1179,13 @@ class MoeRoutingReplayController:
             for ci in dict.fromkeys(cur.plan):
                 route = self._routes.routers[rk].calls[ci]
                 by_k.setdefault(route.max_topk, []).append((rk, ci, route))
+        dev = self._device_for_targets()
         for k, entries in by_k.items():
-            table = self._upload(torch.cat([r.expert_indices for _, _, r in entries]))
+            if all(r.expert_indices.device == dev for _, _, r in entries):
+                for rk, ci, route in entries:     # loaded straight into device tables
+                    self._tables[(rk, ci)] = route.expert_indices
+                continue
+            table = self._upload(torch.cat([r.expert_indices.cpu() for _, _, r in entries]))
             base = 0
             for rk, ci, route in entries:
                 n = route.num_global_tokens

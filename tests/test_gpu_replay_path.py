@@ -199,3 +199,101 @@ def test_device_targets_with_uidless_tokens_equal_host_targets(device, tmp_path)
     p = int(torch.nonzero(a < 0)[0])
     want = random.Random(1 * 1_000_003 + 1 * 97_003 + (p + 1) * 1_299_709).sample(range(e), k)
     assert host[0][0][p].tolist() == want
+
+
+def test_aligned_vllm_routes_replay_bit_exact(device, tmp_path):
+    """vLLM route capture end to end: routes aligned from two choices' vLLM
+    metadata, packed with a shared prompt, built into a bundle, written, read
+    back straight into device route tables, staged by the controller and
+    replayed by the HIP router: every captured token replays its captured
+    experts bit for bit, in both layers."""
+    import math
+    from art_amd.megatron import routing_replay as RR
+    from art_amd.megatron.router import TopKRouter
+    from art_amd.preprocessing import moe_routing as MR
+    from art_amd.preprocessing.pack import TokenizedResult, packed_tensors_from_tokenized_results
+
+    e, k, n_layers, h = 64, 4, 2, 64
+    g = torch.Generator().manual_seed(21)
+
+    def routes(n):
+        return [[torch.randperm(e, generator=g)[:k].tolist() for _ in range(n_layers)]
+                for _ in range(n)]
+
+    class Choice:
+        def __init__(self, meta):
+            self.model_extra = {MR.ART_MOE_ROUTING_METADATA_KEY: meta}
+
+    prompt = list(range(100, 120))
+    shared = routes(len(prompt))
+    results = []
+    for j, completion in enumerate([[7, 8, 9, 10, 11], [7, 8, 12, 13]]):
+        meta = {"prompt_token_ids": prompt, "completion_token_ids": completion,
+                "prompt_routed_experts": shared, "completion_routed_experts": routes(len(completion))}
+        ids = prompt + completion
+        aligned, stats = MR.align_choice_routes_to_tokenized_result(
+            token_ids=ids, choices=[Choice(meta)], choice_offsets=[len(prompt)],
+            choice_token_lengths=[len(completion)])
+        assert stats.routed_tokens == len(ids) and aligned[len(prompt)] == \
+            meta["completion_routed_experts"][0]
+        n, pl = len(ids), len(prompt)
+        results.append(TokenizedResult(token_ids=ids, input_pos=list(range(n)),
+                                       assistant_mask=[0] * pl + [1] * (n - pl),
+                                       logprobs=[math.nan] * pl + [-1.0] * (n - pl),
+                                       advantage=1.0 + j, prompt_id=5, prompt_length=pl,
+                                       moe_routed_experts=aligned))
+    packed = packed_tensors_from_tokenized_results(results, seq_len=64, pad_token_id=0,
+                                                   truncate_long_results=False,
+                                                   include_moe_routing=True)
+    rr = packed["moe_routing_replay"]
+    assert rr.pack_stats.prefix_tree_rows == len(prompt) - 1       # shared but the last
+    assert rr.pack_stats.prefix_tree_conflict_slots == 0
+    bundle = RR.build_moe_routing_replay_bundle_from_packed_tensors(
+        packed_tensors=packed, global_grad_accumulation_sequences=1,
+        topology=RR.ParallelTopology(tp=1, ep=1))
+    bundle.to_dir(tmp_path)
+    on_host = RR.MoeRoutingReplayBundle.from_dir(tmp_path)
+    on_dev = RR.MoeRoutingReplayBundle.from_dir(tmp_path, device=device)
+    keys = [f"chunk_00.layer_{i:04d}.mlp.router" for i in range(n_layers)]
+    for rk in keys:
+        a = on_host.steps[0].routers[rk].calls[0].expert_indices
+        b = on_dev.steps[0].routers[rk].calls[0].expert_indices
+        assert b.device.type == "cuda" and torch.equal(a, b.cpu())
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.decoder = torch.nn.Module()
+            self.decoder.layers = torch.nn.ModuleList()
+            for _ in keys:
+                layer = torch.nn.Module()
+                layer.mlp = torch.nn.Module()
+                layer.mlp.router = TopKRouter(h, e, k, moe_enable_routing_replay=True,
+                                              device=device)
+                self.decoder.layers.append(layer)
+
+    model = Model()
+    ctl = RR.MoeRoutingReplayController(bundle=on_dev, strict=True, device=device,
+                                        device_targets=True)
+    ctl.install_router_patches([model])
+    ctl.set_step(step_index=0, sample_index=[0])
+    ctl.begin_micro(0, 0)
+    seq = int(packed["tokens"].shape[1])
+    ctl.set_local_input_token_uids(torch.arange(seq))
+    captured = rr.token_mask[0]
+    logits = torch.randn(seq, e, generator=g).to(device)
+    for li, layer in enumerate(model.decoder.layers):
+        r = layer.mlp.router
+        probs, rmap = r.routing(logits)
+        tgt = r.router_replay.target_topk_idx
+        assert isinstance(tgt, RR.DeviceReplayTarget)
+        got = tgt.materialize().cpu()
+        want = rr.expert_indices[0, :, li, :].long()
+        assert torch.equal(got[captured], want[captured])
+        assert torch.equal(got, on_host.steps[0].routers[keys[li]].calls[0].expert_indices.long())
+        exp_map = torch.zeros((seq, e), dtype=torch.bool)
+        exp_map[torch.arange(seq).unsqueeze(1), got] = True
+        assert torch.equal(rmap.cpu(), exp_map)
+        assert int(r.last_status.item()) == 0
+    ctl.finalize_step()
+    ctl.remove_router_patches()

@@ -1,0 +1,335 @@
+"""vLLM route capture, route packing and the bundle built from packed routes
+(host logic, CPU).
+
+Scenarios and known answers restate the reference's
+tests/unit/test_moe_routing_real_path.py:44-352 (which need openai and the
+full ART trainer): ``_route(seed) = [[s, s+1], [s+2, s+3]]`` routes over
+two layers, prompts shared through the prefix tree, and the bundle rows
+``[[0, 1], [10, 11], [20, 21]]``.  A choice is any object with a
+``model_extra`` dict (openai's ``Choice`` is one).  Further checks pin what
+those tests leave open: the base64 ``.npy`` form vLLM may send, the one
+``routed_experts`` field over prompt + completion (one route short at the
+end), overlap conflict counts, and the packer's layout against a brute-force
+restatement of the prefix-tree rules.
+"""
+import base64
+import io
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from art_amd.megatron import routing_replay as RR
+from art_amd.preprocessing import moe_routing as MR
+from art_amd.preprocessing.pack import (TokenizedResult, packed_tensors_from_tokenized_results,
+                                        plan_prefix_tree)
+
+TOPO = RR.ParallelTopology(tp=1, ep=1, etp=1, dp=1, sp=False, cp=1, pp=1, vpp=1)
+
+
+class _Choice:
+    def __init__(self, extra=None):
+        self.model_extra = dict(extra or {})
+
+
+def _choice(meta):
+    return _Choice({MR.ART_MOE_ROUTING_METADATA_KEY: meta})
+
+
+def _route(seed):
+    return [[seed, seed + 1], [seed + 2, seed + 3]]
+
+
+def _tokenized(token_ids, routes, *, prompt_id, prompt_length, trainable_start=None,
+               advantage=1.0, weight=1.0):
+    ts = prompt_length if trainable_start is None else trainable_start
+    n = len(token_ids)
+    return TokenizedResult(token_ids=token_ids, input_pos=list(range(n)),
+                           assistant_mask=[0] * ts + [1] * (n - ts),
+                           logprobs=[math.nan] * ts + [-1.0] * (n - ts), advantage=advantage,
+                           weight=weight, prompt_id=prompt_id, prompt_length=prompt_length,
+                           moe_routed_experts=routes, choice_offsets=[ts])
+
+
+# ------------------------------------------------------------ alignment
+def test_align_maps_vllm_routes():
+    routes, stats = MR.align_choice_routes_to_tokenized_result(
+        token_ids=[10, 11, 20, 21],
+        choices=[_choice({"prompt_token_ids": [10, 11], "completion_token_ids": [20, 21],
+                          "prompt_routed_experts": [_route(0), _route(10)],
+                          "completion_routed_experts": [_route(20), _route(30)]})],
+        choice_offsets=[2], choice_token_lengths=[2])
+    assert routes == [_route(0), _route(10), _route(20), _route(30)]
+    assert stats.choices_with_routing == 1 and stats.routed_tokens == 4
+
+
+def test_align_uses_current_vllm_contract():
+    payload = {"prompt_token_ids": [10, 11], "prompt_routed_experts": [_route(0), _route(10)],
+               "choices": [{"index": 0, "finish_reason": "stop",
+                            "message": {"role": "assistant", "content": "x"},
+                            "token_ids": [20, 21], "routed_experts": [_route(20), _route(30)]}]}
+    choice = _Choice({k: v for k, v in payload["choices"][0].items()
+                      if k not in ("index", "finish_reason", "message", "token_ids",
+                                   "routed_experts")})
+    MR.attach_moe_routing_metadata_to_choice(choice=choice, response_payload=payload,
+                                             choice_index=0)
+    meta = choice.model_extra[MR.ART_MOE_ROUTING_METADATA_KEY]
+    assert meta["token_ids"] == [20, 21] and meta["prompt_token_ids"] == [10, 11]
+    routes, stats = MR.align_choice_routes_to_tokenized_result(
+        token_ids=[10, 11, 20, 21], choices=[choice], choice_offsets=[2],
+        choice_token_lengths=[2])
+    assert routes == [_route(0), _route(10), _route(20), _route(30)]
+    assert stats.choices_with_routing == 1 and stats.routed_tokens == 4
+
+
+def test_align_rejects_token_mismatch():
+    with pytest.raises(RuntimeError, match="prompt token ids do not match"):
+        MR.align_choice_routes_to_tokenized_result(
+            token_ids=[10, 12, 20],
+            choices=[_choice({"prompt_token_ids": [10, 11], "completion_token_ids": [20],
+                              "prompt_routed_experts": [_route(0), _route(10)],
+                              "completion_routed_experts": [_route(20)]})],
+            choice_offsets=[2], choice_token_lengths=[1])
+    with pytest.raises(RuntimeError, match="completion token ids do not match"):
+        MR.align_choice_routes_to_tokenized_result(
+            token_ids=[10, 11, 21],
+            choices=[_choice({"prompt_token_ids": [10, 11], "completion_token_ids": [20],
+                              "prompt_routed_experts": [_route(0), _route(10)],
+                              "completion_routed_experts": [_route(20)]})],
+            choice_offsets=[2], choice_token_lengths=[1])
+
+
+def test_align_single_routed_experts_field_base64_npy_and_short_completion():
+    # one routed_experts array over prompt + completion, as a base64 .npy,
+    # one route short at the end (vLLM runs no forward for the last token)
+    arr = np.asarray([_route(0), _route(10), _route(20)], dtype=np.int32)
+    buf = io.BytesIO()
+    np.save(buf, arr, allow_pickle=False)
+    meta = {"prompt_token_ids": [10, 11], "output_token_ids": [20, 21],
+            "routed_experts": base64.b64encode(buf.getvalue()).decode()}
+    routes, stats = MR.align_choice_routes_to_tokenized_result(
+        token_ids=[10, 11, 20, 21], choices=[_Choice(meta)], choice_offsets=[2],
+        choice_token_lengths=[2])
+    assert routes == [_route(0), _route(10), _route(20), None]
+    assert stats.routed_tokens == 3
+    with pytest.raises(RuntimeError, match="routed_experts length does not match"):
+        MR.align_choice_routes_to_tokenized_result(
+            token_ids=[10, 11, 20, 21, 22],
+            choices=[_Choice(dict(meta, output_token_ids=[20, 21, 22]))],
+            choice_offsets=[2], choice_token_lengths=[3])
+    with pytest.raises(RuntimeError, match="Failed to decode routed_experts"):
+        MR.align_choice_routes_to_tokenized_result(
+            token_ids=[10], choices=[_Choice({"prompt_token_ids": [], "token_ids": [10],
+                                              "routed_experts": "not base64 npy"})],
+            choice_offsets=[0], choice_token_lengths=[1])
+
+
+def test_align_overlapping_choices_count_conflicts_and_keep_first():
+    # two choices of one conversation: the second re-sends the shared prefix
+    # with one layer routed differently on token 1
+    a = {"prompt_token_ids": [10, 11], "completion_token_ids": [20],
+         "prompt_routed_experts": [_route(0), _route(10)],
+         "completion_routed_experts": [_route(20)]}
+    b = {"prompt_token_ids": [10, 11, 20], "completion_token_ids": [30],
+         "prompt_routed_experts": [_route(0), [[10, 11], [7, 7]], _route(20)],
+         "completion_routed_experts": [_route(40)]}
+    routes, stats = MR.align_choice_routes_to_tokenized_result(
+        token_ids=[10, 11, 20, 30], choices=[_choice(a), _choice(b)], choice_offsets=[2, 3],
+        choice_token_lengths=[1, 1])
+    assert routes == [_route(0), _route(10), _route(20), _route(40)]
+    assert stats.choices_with_routing == 2 and stats.routed_tokens == 4
+    assert stats.overlap_compared_slots == 12            # 3 shared tokens x 4 slots
+    assert stats.overlap_conflict_slots == 2 and stats.overlap_conflict_rows == 1
+    # brute force over the slots agrees
+    old = [_route(0), _route(10), _route(20)]
+    new = b["prompt_routed_experts"]
+    pairs = [MR.count_route_slot_conflicts(x, y) for x, y in zip(old, new)]
+    assert sum(c for c, _ in pairs) == 12 and sum(d for _, d in pairs) == 2
+
+
+def test_align_mixed_routed_and_unrouted_choices_fail():
+    routed = _choice({"prompt_token_ids": [10], "completion_token_ids": [20],
+                      "prompt_routed_experts": [_route(0)],
+                      "completion_routed_experts": [_route(1)]})
+    with pytest.raises(RuntimeError, match="Some trainable choices had MoE routes"):
+        MR.align_choice_routes_to_tokenized_result(
+            token_ids=[10, 20, 21], choices=[routed, _Choice()], choice_offsets=[1, 2],
+            choice_token_lengths=[1, 1])
+    none, stats = MR.align_choice_routes_to_tokenized_result(
+        token_ids=[10, 20], choices=[_Choice()], choice_offsets=[1], choice_token_lengths=[1])
+    assert none is None and stats.choices_with_routing == 0
+
+
+def test_route_shape_rules():
+    with pytest.raises(RuntimeError, match="topk must be constant"):
+        MR.count_route_slot_conflicts([[1, 2], [3]], [[1, 2], [3, 4]])
+    with pytest.raises(RuntimeError, match="zero layers"):
+        MR.count_route_slot_conflicts([], [[1]])
+    with pytest.raises(RuntimeError, match="different shapes"):
+        MR.count_route_slot_conflicts([[1, 2]], [[1, 2], [3, 4]])
+    assert MR.count_route_slot_conflicts(_route(0), _route(0)) == (4, 0)
+
+
+# ---------------------------------------------------------------- packing
+def test_pack_carries_routes_through_prefix_tree_splicing():
+    first = _tokenized([10, 11, 20, 21], [_route(0), _route(10), _route(20), _route(30)],
+                       prompt_id=123, prompt_length=1, trainable_start=2)
+    second = _tokenized([10, 11, 22, 23], [_route(99), _route(10), _route(40), _route(50)],
+                        prompt_id=123, prompt_length=1, trainable_start=2)
+    packed = packed_tensors_from_tokenized_results([first, second], seq_len=8, pad_token_id=0,
+                                                   truncate_long_results=False,
+                                                   include_moe_routing=True)
+    assert packed["tokens"].tolist()[0][:7] == [10, 11, 20, 21, 11, 22, 23]
+    rr = packed["moe_routing_replay"]
+    assert rr.expert_indices.tolist()[0][:7] == [_route(0), _route(10), _route(20), _route(30),
+                                                 _route(10), _route(40), _route(50)]
+    assert rr.token_mask.tolist()[0] == [True] * 7 + [False]
+    st = rr.pack_stats
+    assert st.prefix_tree_rows == 1 and st.prefix_tree_conflict_rows == 1
+    assert st.prefix_tree_conflict_slots == 4 and st.prefix_tree_compared_slots == 4
+    assert st.packed_tokens == 7
+
+
+def test_pack_keeps_trainable_duplicates_in_leaf_metadata():
+    first = _tokenized([10, 11, 20, 21], [_route(0), _route(10), _route(20), _route(30)],
+                       prompt_id=123, prompt_length=1, trainable_start=2, advantage=2.0,
+                       weight=0.5)
+    second = _tokenized([10, 11, 20, 22], [_route(0), _route(10), _route(40), _route(50)],
+                        prompt_id=123, prompt_length=1, trainable_start=2, advantage=4.0,
+                        weight=0.25)
+    packed = packed_tensors_from_tokenized_results([first, second], seq_len=8, pad_token_id=0,
+                                                   truncate_long_results=False)
+    assert packed["tokens"].tolist()[0][:7] == [10, 11, 20, 21, 11, 20, 22]
+    assert packed["input_pos"].tolist()[0][:7] == [0, 1, 2, 3, 1, 2, 3]
+    assert packed["assistant_mask"].tolist()[0][:7] == [False, False, True, True, False, True,
+                                                        True]
+    assert math.isnan(float(packed["logprobs"][0, 1]))
+    assert float(packed["logprobs"][0, 2]) == -1.0 and float(packed["logprobs"][0, 5]) == -1.0
+    assert float(packed["advantages"][0, 2]) != float(packed["advantages"][0, 5])
+    assert float(packed["weights"][0, 2]) != float(packed["weights"][0, 5])
+    assert int(packed["group_ids"][0, 2]) != int(packed["group_ids"][0, 5])
+    assert packed["moe_routing_replay"] is None
+
+
+def test_pack_nested_prefix_tree_layout():
+    results = [
+        _tokenized([10, 11, 20, 101, 201], [_route(i) for i in range(5)], prompt_id=1,
+                   prompt_length=4, trainable_start=4),
+        _tokenized([10, 11, 20, 102, 202], [_route(i) for i in range(5)], prompt_id=2,
+                   prompt_length=4, trainable_start=4),
+        _tokenized([10, 12, 30, 103, 203], [_route(i) for i in range(5)], prompt_id=3,
+                   prompt_length=4, trainable_start=4),
+    ]
+    packed = packed_tensors_from_tokenized_results(results, seq_len=16, pad_token_id=0,
+                                                   truncate_long_results=False)
+    assert packed["tokens"].tolist()[0][:11] == [10, 11, 20, 101, 201, 102, 202, 12, 30, 103, 203]
+    gid, pid = packed["group_ids"][0].tolist(), packed["parent_ids"][0].tolist()
+    # segments: [10] root, [11,20] under it, two leaves under that, then the
+    # [12,30,103,203] branch under the root: depth 2 below the root
+    assert gid[:11] == [1, 2, 2, 3, 3, 4, 4, 5, 5, 5, 5]
+    assert pid[:11] == [1, 1, 1, 2, 2, 2, 2, 1, 1, 1, 1]
+    assert gid[11:] == [-1] * 5 and pid[11:] == [-1] * 5
+    m = packed["assistant_mask"][0]
+    assert not m[2] and not m[3] and m[4] and m[6]
+    assert gid[4] != gid[6]
+
+
+def test_pack_infers_at_least_topk_experts_from_sparse_routes():
+    result = _tokenized([10, 20], [[[0, 0, 0, 0]], [[0, 0, 0, 0]]], prompt_id=456,
+                        prompt_length=1)
+    packed = packed_tensors_from_tokenized_results([result], seq_len=4, pad_token_id=0,
+                                                   truncate_long_results=False,
+                                                   include_moe_routing=True)
+    rr = packed["moe_routing_replay"]
+    assert rr.topk == 4 and rr.num_experts == 4 and rr.num_layers == 1
+    with pytest.raises(RuntimeError, match="no aligned routed experts"):
+        packed_tensors_from_tokenized_results(
+            [_tokenized([10, 20], None, prompt_id=1, prompt_length=1)], seq_len=4,
+            include_moe_routing=True)
+
+
+def test_build_replay_bundle_uses_packed_sequence_sample_calls():
+    result = _tokenized([10, 11, 20], [_route(0), _route(10), _route(20)], prompt_id=456,
+                        prompt_length=2)
+    packed = packed_tensors_from_tokenized_results([result], seq_len=4, pad_token_id=0,
+                                                   truncate_long_results=False,
+                                                   include_moe_routing=True)
+    bundle = RR.build_moe_routing_replay_bundle_from_packed_tensors(
+        packed_tensors=packed, global_grad_accumulation_sequences=1, topology=TOPO)
+    route = bundle.steps[0].routers["chunk_00.layer_0000.mlp.router"].calls[0]
+    assert route.sample_index == 0
+    rows = route.expert_indices.tolist()
+    assert rows[:3] == [[0, 1], [10, 11], [20, 21]]
+    assert len(set(rows[3])) == 2
+    seed = 1 * 1_000_003 + 1 * 97_003
+    assert rows[3] == random.Random(seed + 4 * 1_299_709).sample(range(24), 2)
+    layer1 = bundle.steps[0].routers["chunk_00.layer_0001.mlp.router"].calls[0]
+    assert layer1.expert_indices.tolist()[:3] == [[2, 3], [12, 13], [22, 23]]
+
+
+def _brute_force_segments(rows, share, max_depth):
+    """The prefix-tree rules restated as a plain recursion (own reading of
+    prefix_tree_packing.py:163-256)."""
+    out = []
+
+    def emit(seqs, a, b, parent):
+        gid = len(out) + 1
+        out.append((tuple(seqs), a, b, gid, gid if parent is None else parent))
+        return gid
+
+    def walk(members, start, parent, depth):
+        live = [i for i in members if len(rows[i]) > start]
+        sh = [i for i in live if share[i] > start]
+        for i in live:
+            if i not in sh:
+                emit((i,), start, len(rows[i]), parent)
+        if not sh:
+            return
+        if max_depth == 0 or len(sh) == 1 or (parent is not None and depth >= max_depth):
+            for i in sh:
+                emit((i,), start, len(rows[i]), parent)
+            return
+        end = start
+        while end < min(min(len(rows[i]), share[i]) for i in sh) and \
+                len({rows[i][end] for i in sh}) == 1:
+            end += 1
+        if end > start:
+            walk(sh, end, emit(sh, start, end, parent), depth + 1)
+            return
+        order = []
+        for i in sh:
+            if rows[i][start] not in order:
+                order.append(rows[i][start])
+        for tok in order:
+            walk([i for i in sh if rows[i][start] == tok], start, parent, depth)
+
+    walk(list(range(len(rows))), 0, None, 0)
+    return out
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_prefix_tree_plan_matches_brute_force(seed):
+    rng = random.Random(seed)
+    rows = [tuple(rng.choice([1, 2, 3]) for _ in range(rng.randint(0, 9)))
+            for _ in range(rng.randint(1, 7))]
+    share = [rng.randint(0, len(r)) for r in rows]
+    for depth in (0, 1, 2, 16):
+        got = [(s.sequences, s.start, s.end, s.group_id, s.parent_id)
+               for s in plan_prefix_tree(rows, max_depth=depth, shareable=share)]
+        assert got == _brute_force_segments(rows, share, depth), (rows, share, depth)
+
+
+def test_tensorize_routes_rejects_ragged_and_empty():
+    with pytest.raises(RuntimeError, match="No MoE routes were packed"):
+        MR.tensorize_moe_routes([[None, None]], 4)
+    with pytest.raises(RuntimeError, match="one rectangular shape"):
+        MR.tensorize_moe_routes([[_route(0), [[1, 2]]]], 4)
+    idx, mask, n_layers, k, e = MR.tensorize_moe_routes([[_route(5), None], [None]], 3)
+    assert idx.dtype == torch.int32 and idx.shape == (2, 3, 2, 2)
+    assert mask.tolist() == [[True, False, False], [False, False, False]]
+    assert (n_layers, k, e) == (2, 2, 9)
+    with pytest.raises(RuntimeError, match="topk cannot exceed num_experts"):
+        MR.PackedMoeRoutingReplay(expert_indices=idx, token_mask=mask, num_layers=2, topk=2,
+                                  num_experts=1)
