@@ -16,8 +16,20 @@ megatron's mask-based permute produces (``arange(T).expand(E, T)
 .masked_select(routing_map.T)``, canonicalised in trace.py:181-232).
 Row data of bf16 hidden states (H % 8 == 0) moves through the HIP gather /
 combine kernels; other dtypes (token uids, fp32 metadata) through torch
-indexing on the same device.  Capacity dropping (``drop_and_pad=True``) is
-not supported.
+indexing on the same device.
+
+Capacity layout (``drop_and_pad=True``), restating megatron-core 0.17.0's
+``moe_utils.permute`` / ``unpermute`` (a dependency of the reference that is
+not vendored; the call site is trace.py:390-398): every expert gets exactly
+``capacity = num_out_tokens // E`` rows (at most T); expert e's block holds
+the tokens routed to it in ascending order, the ones past the capacity
+dropped, then tokens NOT routed to it, again ascending, as padding.
+``permuted_probs`` are the dense probabilities at those (token, expert)
+pairs, so padding rows carry 0; ``unpermute`` weights rows by them (or sums
+unweighted without ``probs``) and adds each row back to its token.  Here the
+layout is a [T, E] slot map (the row of token t in expert e's block, or -1)
+driving the same HIP gather and fixed-order fp32 combine.  ``pad_offsets``
+(the fused-padding variant) is not supported.
 """
 from __future__ import annotations
 
@@ -84,12 +96,70 @@ class _UnpermuteFn(torch.autograd.Function):
         return d_rows, None, d_wgt
 
 
+def _capacity_slots(sorted_indices: torch.Tensor, num_tokens: int, num_experts: int,
+                    capacity: int) -> torch.Tensor:
+    """[T, E] int32: the row of token t in expert e's capacity block, or -1."""
+    slots = torch.full((num_tokens, num_experts), -1, dtype=torch.int32,
+                       device=sorted_indices.device)
+    rows = torch.arange(num_experts * capacity, device=sorted_indices.device)
+    slots[sorted_indices.long(), rows // capacity] = rows.to(torch.int32)
+    return slots
+
+
+class _CapacityCombineFn(torch.autograd.Function):
+    """y[t] = sum_e w[t, e] rows[slots[t, e]] over a capacity layout
+    (w None: 1); rows [E*cap, H]."""
+
+    @staticmethod
+    def forward(ctx, rows, slots, src, wgt):
+        ctx.save_for_backward(rows, slots, src, wgt)
+        return ops.combine(rows.contiguous(), slots, slots.shape[0], wgt=wgt)
+
+    @staticmethod
+    def backward(ctx, dy):
+        rows, slots, src, wgt = ctx.saved_tensors
+        dy = dy.contiguous()
+        d_rows = ops.permute(dy, slots, rows.shape[0])
+        d_wgt = None
+        if wgt is not None:
+            cap = rows.shape[0] // slots.shape[1]
+            expert = torch.arange(rows.shape[0], device=rows.device) // cap
+            w_row = wgt[src.long(), expert]
+            dot = (rows.float() * dy.float().index_select(0, src.long())).sum(-1)
+            d_wgt = torch.zeros_like(wgt)
+            d_wgt[src.long(), expert] = dot
+            d_rows = (d_rows.float() * w_row.unsqueeze(1)).to(d_rows.dtype)
+        return d_rows, None, None, d_wgt
+
+
+def _permute_capacity(tokens, routing_map, probs, num_out_tokens):
+    t, e = routing_map.shape
+    if num_out_tokens is None:
+        raise ValueError("permute: drop_and_pad needs num_out_tokens (E x capacity)")
+    cap = min(int(num_out_tokens) // e, t)
+    if t == 0 or cap == 0:
+        empty = tokens.new_zeros((0, *tokens.shape[1:]))
+        return (tokens.sum() * 0 + empty if tokens.is_floating_point() else empty,
+                None if probs is None else probs.new_zeros((0,)),
+                torch.zeros(0, dtype=torch.int64, device=tokens.device))
+    # routed tokens first (ascending), then the others (ascending), per expert
+    order = routing_map.to(torch.int8).t().argsort(dim=1, descending=True, stable=True)[:, :cap]
+    sorted_indices = order.reshape(-1).contiguous()
+    if _hip_rows(tokens):
+        slots = _capacity_slots(sorted_indices, t, e, cap)
+        out = _PermuteFn.apply(tokens, slots, e * cap)
+    else:
+        out = tokens.index_select(0, sorted_indices)
+    permuted_probs = None if probs is None else probs.t().gather(1, order).reshape(-1)
+    return out, permuted_probs, sorted_indices
+
+
 def permute(tokens: torch.Tensor, routing_map: torch.Tensor, probs: torch.Tensor | None = None,
             num_out_tokens: int | None = None, fused: bool = False, drop_and_pad: bool = False):
     """(permuted_tokens [M, H], permuted_probs [M] or None, sorted_indices [M] int64)."""
     del fused
     if drop_and_pad:
-        raise ValueError("permute: drop_and_pad (expert capacity) is not supported")
+        return _permute_capacity(tokens, routing_map, probs, num_out_tokens)
     t, e = routing_map.shape
     k = _k_per_token(routing_map, num_out_tokens)
     if t == 0 or k == 0:
@@ -118,9 +188,9 @@ def unpermute(permuted_tokens: torch.Tensor, sorted_indices: torch.Tensor, resto
               pad_offsets: torch.Tensor | None = None) -> torch.Tensor:
     """Scatter-add the permuted rows back to their tokens (weighted by ``probs``
     [T, E] at the routed positions when given)."""
-    del fused, pad_offsets
-    if drop_and_pad:
-        raise ValueError("unpermute: drop_and_pad (expert capacity) is not supported")
+    del fused
+    if pad_offsets is not None:
+        raise ValueError("unpermute: pad_offsets (fused padded layouts) is not supported")
     shape = tuple(int(d) for d in restore_shape)
     if permuted_tokens.numel() == 0:
         zero = permuted_tokens.sum() * 0.0 + sorted_indices.sum().to(permuted_tokens) * 0.0
@@ -128,6 +198,25 @@ def unpermute(permuted_tokens: torch.Tensor, sorted_indices: torch.Tensor, resto
             zero = zero + probs.to(permuted_tokens.dtype).sum() * 0.0
         return zero.expand(shape).clone()
     t = shape[0]
+    if drop_and_pad:
+        if routing_map is None:
+            raise ValueError("unpermute: drop_and_pad needs the routing_map (for E)")
+        e = routing_map.shape[1]
+        m = sorted_indices.numel()
+        if m % e:
+            raise ValueError(f"unpermute: {m} capacity rows do not split over {e} experts")
+        cap = m // e
+        src = sorted_indices.to(torch.int32).contiguous()
+        wgt = None if probs is None else probs.float().contiguous()
+        if _hip_rows(permuted_tokens):
+            slots = _capacity_slots(sorted_indices, t, e, cap)
+            return _CapacityCombineFn.apply(permuted_tokens, slots, src, wgt).view(shape)
+        rows = permuted_tokens
+        if wgt is not None:
+            expert = torch.arange(m, device=rows.device) // cap
+            rows = rows * wgt[sorted_indices.long(), expert].unsqueeze(-1).to(rows.dtype)
+        out = permuted_tokens.new_zeros((t, *permuted_tokens.shape[1:]))
+        return out.index_add(0, sorted_indices.long(), rows).view(shape)
     m = sorted_indices.numel()
     if m % t:
         raise ValueError("unpermute needs the same number of rows for every token")

@@ -280,7 +280,8 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
 }
 
 // ---------------------------------------------------------- permute / combine
-// One wavefront per token; rows move as 16-byte chunks of 8 bf16.
+// One wavefront per token; rows move as 16-byte chunks of 8 bf16.  A token's
+// destination slots are read 64 at a time (one per lane) and broadcast.
 __global__ __launch_bounds__(256) void permute_kernel(const U4 *__restrict__ x,
                                                       const int32_t *__restrict__ dest,
                                                       int64_t T, int k, int H8,
@@ -297,20 +298,25 @@ __global__ __launch_bounds__(256) void permute_kernel(const U4 *__restrict__ x,
       const int c = c0 + u * kWave + lane;
       if (c < H8) v[u] = src[c];
     }
-    for (int j = 0; j < k; ++j) {
-      const int d = __shfl(my_dest, j, kWave);
-      if (d < 0) continue;
-      U4 *dst = xp + (int64_t)d * H8;
+    for (int j0 = 0; j0 < k; j0 += kWave) {
+      const int md = j0 == 0 ? my_dest : (j0 + lane < k ? dest[t * k + j0 + lane] : -1);
+      const int kb = k - j0 < kWave ? k - j0 : kWave;
+      for (int j = 0; j < kb; ++j) {
+        const int d = __shfl(md, j, kWave);
+        if (d < 0) continue;
+        U4 *dst = xp + (int64_t)d * H8;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int c = c0 + u * kWave + lane;
-        if (c < H8) dst[c] = v[u];
+        for (int u = 0; u < 4; ++u) {
+          const int c = c0 + u * kWave + lane;
+          if (c < H8) dst[c] = v[u];
+        }
       }
     }
   }
 }
 
-constexpr int kMaxK = 32;
+constexpr int kMaxK = 32;        // top-k of the router kernels
+constexpr int kMaxSlots = 1024;  // slots per token of permute / combine (capacity layouts: E)
 
 __global__ __launch_bounds__(256) void combine_kernel(
     const U4 *__restrict__ yp, const int32_t *__restrict__ dest, const float *__restrict__ wgt,
@@ -325,9 +331,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
   if (t >= T) return;
   const int c0 = (int)(wv - t * n_chunks) * kWave;
   const bool act = lane < k;
-  const int my_dest = act ? dest[t * k + lane] : -1;
-  const float my_w = (act && wgt) ? wgt[t * k + lane] : 1.0f;
-  const int my_e = (act && w_r) ? idx[t * k + lane] : -1;
+  const int my_e = (act && w_r) ? idx[t * k + lane] : -1;     // w_r: k <= 32
   const float my_dl = (act && w_r) ? dl[t * k + lane] : 0.0f;
   // Every lane of the wavefront runs the slot loops (uniform), so the slot
   // broadcasts below always read active lanes.  Slots go in blocks of 8
@@ -340,23 +344,29 @@ __global__ __launch_bounds__(256) void combine_kernel(
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int jb = 0; jb < k; jb += 8) {
-      U4 v[8];
-      int dj[8];
-      float wj[8];
+    for (int j0 = 0; j0 < k; j0 += kWave) {      // slots 64 at a time, one per lane
+      const int kb = k - j0 < kWave ? k - j0 : kWave;
+      const bool a = lane < kb;
+      const int my_dest = a ? dest[t * k + j0 + lane] : -1;
+      const float my_w = (a && wgt) ? wgt[t * k + j0 + lane] : 1.0f;
+      for (int jb = 0; jb < kb; jb += 8) {
+        U4 v[8];
+        int dj[8];
+        float wj[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        dj[u] = __shfl(my_dest, jb + u, kWave);
-        wj[u] = __shfl(my_w, jb + u, kWave);
-        v[u] = (dj[u] >= 0 && on) ? yp[(int64_t)dj[u] * H8 + c] : U4{0u, 0u, 0u, 0u};
-      }
+        for (int u = 0; u < 8; ++u) {
+          dj[u] = __shfl(my_dest, jb + u, kWave);
+          wj[u] = __shfl(my_w, jb + u, kWave);
+          v[u] = (dj[u] >= 0 && on) ? yp[(int64_t)dj[u] * H8 + c] : U4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (dj[u] < 0) continue;
-        float f[8];
-        unpack8(v[u], f);
+        for (int u = 0; u < 8; ++u) {
+          if (dj[u] < 0) continue;
+          float f[8];
+          unpack8(v[u], f);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += wj[u] * f[i];
+          for (int i = 0; i < 8; ++i) acc[i] += wj[u] * f[i];
+        }
       }
     }
     if (w_r) {
@@ -866,8 +876,8 @@ extern "C" int art_moe_segments_from_counts(const int64_t *counts, int32_t E, in
 extern "C" int art_moe_permute(const void *x, const int32_t *dest, int64_t T, int32_t k,
                                int32_t H, void *x_perm, void *stream) {
   clear_error();
-  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0,
-              "permute: need H %% 8 == 0 and 1 <= k <= 32 (H=%d k=%d)", H, k);
+  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxSlots && H > 0 && H % 8 == 0,
+              "permute: need H %% 8 == 0 and 1 <= k <= 1024 (H=%d k=%d)", H, k);
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(x && dest && x_perm, "permute: null pointer");
   permute_kernel<<<dim3((unsigned)((T + 3) / 4)), 256, 0, as_stream(stream)>>>(
@@ -880,8 +890,9 @@ extern "C" int art_moe_combine(const void *y_perm, const int32_t *dest, const fl
                                const void *addend, int64_t T, int32_t k, int32_t H, void *y,
                                void *stream) {
   clear_error();
-  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxK && H > 0 && H % 8 == 0,
-              "combine: need H %% 8 == 0 and 1 <= k <= 32 (H=%d k=%d)", H, k);
+  ART_REQUIRE(T >= 0 && k >= 1 && k <= kMaxSlots && H > 0 && H % 8 == 0,
+              "combine: need H %% 8 == 0 and 1 <= k <= 1024 (H=%d k=%d)", H, k);
+  ART_REQUIRE(!w_r || k <= kMaxK, "combine: the router-gradient term needs k <= 32 (k=%d)", k);
   if (T == 0) return ART_MOE_OK;
   ART_REQUIRE(y_perm && dest && y && (!w_r || (dl && idx)), "combine: null pointer");
   const int n_chunks = (H / 8 + kWave - 1) / kWave;

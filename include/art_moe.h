@@ -164,7 +164,9 @@ int art_moe_segments_from_counts(const int64_t *counts, int32_t E, int32_t *seg,
 
 /* -------------------------------------------------------- permute/combine */
 
-/* x_perm[dest[t,j], :] = x[t, :] for bf16 rows of H (H % 8 == 0).
+/* x_perm[dest[t,j], :] = x[t, :] for bf16 rows of H (H % 8 == 0), j < k <=
+ * 1024; dest < 0 skips the slot.  k = E gives megatron's capacity layout
+ * (drop_and_pad: dest[t,e] = the row of token t in expert e's block, or -1).
  * Replaces: moe_utils.permute (tokens gather). */
 int art_moe_permute(const void *x, const int32_t *dest, int64_t T, int32_t k,
                     int32_t H, void *x_perm, void *stream);
@@ -172,7 +174,8 @@ int art_moe_permute(const void *x, const int32_t *dest, int64_t T, int32_t k,
 /* y[t, :] = sum_j (wgt ? wgt[t,j] : 1) * y_perm[dest[t,j], :]
  *           + (w_r ? sum_j dl[t,j] * w_r[idx[t,j], :] : 0)
  *           + (addend ? addend[t, :] : 0)
- * fp32 accumulation in slot order j = 0..k-1, then the router term, then the
+ * fp32 accumulation in slot order j = 0..k-1 (k <= 1024; dest < 0 skips the
+ * slot; the router term needs k <= 32), then the router term, then the
  * addend; bf16 out (one rounding).  With w_r == NULL this is
  * moe_utils.unpermute (combine); with w_r it also adds the router input
  * gradient dl @ W_r restricted to the k selected experts; the bf16 [T, H]

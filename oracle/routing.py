@@ -33,6 +33,12 @@ Pinning
   .masked_select(routing_map.T)`` (megatron's own construction), the
   hand-derived KAT from the reference replay test routes
   (tests/golden/routing_kats.json) and a pure-Python loop on small inputs.
+* ``capacity_layout`` (megatron-core 0.17.0 ``moe_utils.permute`` with
+  ``drop_and_pad=True``; megatron-core is a dependency the reference pins in
+  pyproject.toml and does not vendor; call site
+  tests/integration/megatron/routing_replay/trace.py:390-398): a pure-Python
+  per-expert loop on small inputs and the invariants every expert block must
+  satisfy (tests/test_oracle_routing.py).
 """
 from __future__ import annotations
 
@@ -138,3 +144,15 @@ def row_token_closed_form(routing_map: np.ndarray) -> np.ndarray:
     rm_t = np.asarray(routing_map, dtype=bool).T
     tok = np.broadcast_to(np.arange(rm_t.shape[1]), rm_t.shape)
     return tok[rm_t].astype(np.int64)
+
+
+def capacity_layout(routing_map: np.ndarray, capacity: int) -> np.ndarray:
+    """Token of each row of the capacity layout, int64 [E * capacity]:
+    expert e's block lists the tokens routed to e in ascending order, then
+    the tokens not routed to e in ascending order (padding), cut to
+    ``min(capacity, T)`` rows (routed tokens past the capacity are dropped).
+    This is a stable descending sort of each expert's 0/1 column."""
+    rm_t = np.asarray(routing_map, dtype=bool).T           # [E, T]
+    cap = min(int(capacity), rm_t.shape[1])
+    order = np.argsort(~rm_t, axis=1, kind="stable")        # True (routed) first
+    return order[:, :cap].reshape(-1).astype(np.int64)

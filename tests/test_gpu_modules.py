@@ -74,6 +74,53 @@ def test_permute_unpermute_gradients(device):
     assert rel(pr.grad * rmap, prr.grad * rmap.cpu()) < 2e-2
 
 
+@pytest.mark.parametrize("t,e,k,h,cap_factor", [(300, 16, 4, 256, 1.0), (200, 8, 2, 128, 0.5),
+                                                 (64, 4, 4, 24, 1.5)])
+def test_permute_unpermute_capacity_layout(device, t, e, k, h, cap_factor):
+    """drop_and_pad: rows follow the oracle's capacity layout (routed tokens
+    ascending, the excess dropped, then non-routed padding ascending) bit for
+    bit, probs are gathered at those (token, expert) pairs (0 on padding),
+    unpermute sums within one bf16 ulp of an fp32 index_add, and gradients
+    (rows and probs) match an fp32 torch restatement."""
+    from art_amd.megatron.moe_utils import permute, unpermute
+    from oracle import routing as R
+    rmap, probs = _routing(t, e, k, t + 3 * e, device)
+    n_out = int(t * k * cap_factor)
+    cap = min(n_out // e, t)
+    x = torch.randn(t, h, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(device)
+    out, pprobs, sidx = permute(x, rmap, probs=probs, num_out_tokens=n_out, drop_and_pad=True)
+    want = torch.from_numpy(R.capacity_layout(rmap.cpu().numpy(), cap))
+    assert torch.equal(sidx.cpu(), want) and out.shape == (e * cap, h)
+    assert torch.equal(out.cpu(), x.cpu()[want])
+    expert = torch.arange(e * cap) // cap
+    assert torch.equal(pprobs.cpu(), probs.cpu()[want, expert])
+    uids, _, _ = permute(torch.arange(t, device=device).unsqueeze(-1), rmap, num_out_tokens=n_out,
+                         drop_and_pad=True)
+    assert torch.equal(uids.cpu().view(-1), want)
+    y = unpermute(out, sidx, x.shape, routing_map=rmap, drop_and_pad=True)
+    ref = torch.zeros(t, h).index_add(0, want, out.cpu().float())
+    torch.testing.assert_close(y.cpu().float(), ref, rtol=2 ** -8, atol=1e-6)
+    # weighted, with gradients
+    xg = x.clone().requires_grad_()
+    pg = probs.clone().requires_grad_()
+    o2, _, s2 = permute(xg, rmap, num_out_tokens=n_out, drop_and_pad=True)
+    yw = unpermute(o2, s2, x.shape, probs=pg, routing_map=rmap, drop_and_pad=True)
+    refw = torch.zeros(t, h).index_add(0, want, out.cpu().float() *
+                                       probs.cpu()[want, expert].unsqueeze(1))
+    torch.testing.assert_close(yw.detach().cpu().float(), refw, rtol=2 ** -7, atol=1e-5)
+    gy = torch.randn(t, h, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    yw.backward(gy.to(device))
+    xr = x.detach().cpu().float().requires_grad_()
+    prr = probs.cpu().clone().requires_grad_()
+    yr = torch.zeros(t, h).index_add(0, want, xr[want] * prr[want, expert].unsqueeze(1))
+    yr.backward(gy.float())
+    assert rel(xg.grad, xr.grad) < 2e-2
+    assert rel(pg.grad, prr.grad) < 2e-2
+    with pytest.raises(ValueError, match="pad_offsets"):
+        unpermute(out, sidx, x.shape, routing_map=rmap, drop_and_pad=True,
+                  pad_offsets=torch.zeros(e, dtype=torch.int64, device=device))
+
+
 def test_weighted_bias_swiglu_impl(device):
     from art_amd.megatron.moe_utils import weighted_bias_swiglu_impl
     m, f = 1000, 384

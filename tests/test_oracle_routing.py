@@ -124,3 +124,29 @@ def test_replay_rejects_bad_ids():
     idx, w = R.replay(logits, np.array([[3, 1], [0, 2]]))
     assert idx.tolist() == [[3, 1], [0, 2]]
     np.testing.assert_allclose(w, 0.5)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_capacity_layout_matches_per_expert_loop(seed):
+    """The capacity layout against a plain loop: per expert, its routed
+    tokens ascending, then the others ascending, cut to the capacity."""
+    rng = np.random.default_rng(seed)
+    t, e, k = int(rng.integers(1, 40)), int(rng.integers(1, 9)), 0
+    k = int(rng.integers(1, e + 1))
+    idx = np.stack([rng.permutation(e)[:k] for _ in range(t)])
+    rmap = R.routing_map_from_idx(idx, e)
+    for cap in (1, max(1, t * k // e), t, t + 5):
+        got = R.capacity_layout(rmap, cap)
+        want = []
+        for ex in range(e):
+            routed = [tok for tok in range(t) if rmap[tok, ex]]
+            other = [tok for tok in range(t) if not rmap[tok, ex]]
+            want += (routed + other)[:min(cap, t)]
+        assert got.tolist() == want
+        c = min(cap, t)
+        blocks = got.reshape(e, c)
+        for ex in range(e):   # invariants: no repeats; routed prefix = min(count, cap)
+            assert len(set(blocks[ex].tolist())) == c
+            n_routed = int(rmap[:, ex].sum())
+            assert rmap[blocks[ex], ex].tolist() == [True] * min(n_routed, c) + \
+                [False] * (c - min(n_routed, c))
