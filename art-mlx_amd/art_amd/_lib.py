@@ -31,6 +31,7 @@ B_FP8_ROWSCALE = 1
 B_FP8_KSCALE = 2
 AB_FP8 = 3
 F16 = 4
+B_KN = 5        # bf16 weights stored k-major ([E][K][N]): data gradients on the forward layout
 WGRAD_F16 = 16
 
 

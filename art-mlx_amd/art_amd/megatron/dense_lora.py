@@ -152,7 +152,8 @@ class _DenseLoRAFn(torch.autograd.Function):
         for i in range(0, len(items), 16):
             ops.pack(*items[i:i + 16])
         g = ops.grouped_gemm(dy, lt, seg1, 1, m=t)                          # [T, rp]
-        dx = ops.grouped_gemm(dy, lin.weight_t.unsqueeze(0), seg1, 1, m=t, tl=g, l=a_cat_t)
+        dx = ops.grouped_gemm(dy, lin.weight.unsqueeze(0), seg1, 1, m=t, tl=g, l=a_cat_t,
+                              b_kn=True)                              # W [out, in] read k-major
         g_a = _wgrad_rows(x2, g)                                            # [in, rp] fp32
         g_b = _wgrad_rows(dy, tl).t()                                       # [rp, out] fp32 view
         grads = []
@@ -173,7 +174,6 @@ class DenseLoRALinear(torch.nn.Module):
         super().__init__()
         self.out_features, self.in_features = (int(d) for d in weight.shape)
         self.register_buffer("weight", weight.detach().contiguous())
-        self._weight_t: torch.Tensor | None = None
         self.segments = segments
         for i, (lora, pl) in enumerate(segments):
             if lora.A_T.dim() != 2:
@@ -186,12 +186,6 @@ class DenseLoRALinear(torch.nn.Module):
                 raise ValueError(f"segment {i}: placement {pl} does not tile {self.out_features} "
                                  "output columns")
             self.add_module(f"lora{i}", lora)
-
-    @property
-    def weight_t(self) -> torch.Tensor:
-        if self._weight_t is None or self._weight_t.device != self.weight.device:
-            self._weight_t = ops.transposed(self.weight.unsqueeze(0))[0]
-        return self._weight_t
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]

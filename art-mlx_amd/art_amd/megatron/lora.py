@@ -270,8 +270,11 @@ class _GroupedLinearFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         lin, seg = ctx.lin, ctx.seg
-        dx = ops.grouped_gemm(dy.contiguous(), lin.weight_t, seg, lin.num_gemms,
-                              b_scale=lin.weight_scale, scale_per_k=True)
+        if lin.weight_t is None:   # bf16: read W [E, out, in] k-major, dx = dy @ W[e]
+            dx = ops.grouped_gemm(dy.contiguous(), lin.weight, seg, lin.num_gemms, b_kn=True)
+        else:
+            dx = ops.grouped_gemm(dy.contiguous(), lin.weight_t, seg, lin.num_gemms,
+                                  b_scale=lin.weight_scale, scale_per_k=True)
         return dx, None, None
 
 
@@ -280,16 +283,25 @@ class GroupedLinear(torch.nn.Module):
     segments (TE GroupedLinear forward/dgrad; no bias, weights not trained).
 
     ``weight`` [E, out, in] bf16, or fp8 e4m3fn with ``weight_scale`` [E, out].
+    The data gradient reads a bf16 weight in place (k-major) unless
+    ``transposed_copy`` keeps a transposed copy ``weight_t`` (faster when
+    ``in`` is narrow, twice the memory); fp8 weights always keep one (per-k
+    scales there).
     """
 
-    def __init__(self, weight: torch.Tensor, weight_scale: torch.Tensor | None = None) -> None:
+    def __init__(self, weight: torch.Tensor, weight_scale: torch.Tensor | None = None,
+                 transposed_copy: bool = False) -> None:
         super().__init__()
         from ..quant import transpose_fp8
         self.num_gemms, self.out_features, self.in_features = (int(d) for d in weight.shape)
         self.register_buffer("weight", weight.detach().contiguous())
         self.register_buffer("weight_scale", None if weight_scale is None
                              else weight_scale.detach().float().contiguous())
-        wt = transpose_fp8(self.weight) if weight_scale is not None else ops.transposed(self.weight)
+        wt = None
+        if weight_scale is not None:
+            wt = transpose_fp8(self.weight)
+        elif transposed_copy:
+            wt = ops.transposed(self.weight)
         self.register_buffer("weight_t", wt)
 
     def forward(self, x: torch.Tensor, m_splits):

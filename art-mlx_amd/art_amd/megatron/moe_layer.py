@@ -48,15 +48,20 @@ FUSE_PROJECTIONS = os.environ.get("ART_MOE_FUSE_PROJ", "1") != "0"
 
 @dataclass
 class FrozenExperts:
-    """Frozen base weights plus their transposed copies (built once).
+    """Frozen base weights (built once).
 
     w_r [E, H] router weight (None when the caller supplies logits)
     w1  [E, 2F, H] FC1 (TE GroupedLinear ``weight{e}`` layout, gate rows first)
     w2  [E, H, F]  FC2
-    w1t [E, H, 2F], w2t [E, F, H] transposed copies for the data gradients.
-    With fp8 storage (``build_fp8``) w1 / w2 and their copies hold e4m3fn
-    bytes and w1_scale [E, 2F] / w2_scale [E, H] the per-output-row scales
-    (per-k scales of the transposed copies); the products use bf16(q * s).
+    bf16: the FC1 data gradient reads W1 in this layout (k-major B through
+    transposing LDS reads), so there is no W1 copy (w1t None); the FC2 data
+    gradient, where the k-major read costs ~25% more time, keeps a transposed
+    W2 copy w2t [E, F, H] unless built with ``w2_copy=False`` (then it reads
+    W2 k-major too and the frozen weights take no extra memory).
+    With fp8 storage (``build_fp8``) w1 / w2 hold e4m3fn bytes with w1_scale
+    [E, 2F] / w2_scale [E, H] the per-output-row scales, and w1t [E, H, 2F] /
+    w2t [E, F, H] are fp8 transposed copies (per-k scales there) for the data
+    gradients; the products use bf16(q * s).
     ``act_fp8`` (W8A8, opt-in) quantises the activations of the four base
     products to e4m3fn per row too and runs them on the fp8 MFMA: about twice
     the MFMA rate and two thirds of the operand bytes, at ~2.7% relative
@@ -66,18 +71,18 @@ class FrozenExperts:
     w_r: torch.Tensor | None
     w1: torch.Tensor
     w2: torch.Tensor
-    w1t: torch.Tensor
-    w2t: torch.Tensor
+    w1t: torch.Tensor | None
+    w2t: torch.Tensor | None
     w1_scale: torch.Tensor | None = None
     w2_scale: torch.Tensor | None = None
     act_fp8: bool = False
 
     @classmethod
-    def build(cls, w_r, w1, w2) -> "FrozenExperts":
+    def build(cls, w_r, w1, w2, *, w2_copy: bool = True) -> "FrozenExperts":
         w1 = w1.detach().contiguous()
         w2 = w2.detach().contiguous()
-        return cls(w_r.detach().contiguous() if w_r is not None else None,
-                   w1, w2, ops.transposed(w1), ops.transposed(w2))
+        return cls(w_r.detach().contiguous() if w_r is not None else None, w1, w2, None,
+                   ops.transposed(w2) if w2_copy else None)
 
     @classmethod
     def build_fp8(cls, w_r, w1_q, w1_scale, w2_q, w2_scale, act_fp8: bool = False) -> "FrozenExperts":
@@ -317,10 +322,14 @@ class _MoELoRALayerFn(torch.autograd.Function):
             dyq, dys = ops.quantize_rows_fp8(dy, rows=rows, seg=seg, col_scale=base.w2_scale, m=m)
             out = ops.fc2_dgrad_swiglu(dyq, base.w2t, seg, e, y1, row_prob, m=m,
                                        tl=g2, l2=adp, a_scale=dys, proj=proj, proj_split=split)
-        else:
+        elif base.w2t is not None:
             out = ops.fc2_dgrad_swiglu(dy, base.w2t, seg, e, y1, row_prob, m=m,
                                        a_rows=rows, tl=g2, l2=adp,
                                        w2_scale=base.w2_scale, proj=proj, proj_split=split)
+        else:   # W2 [E, H, F] read k-major: dh = dy @ W2[e]
+            out = ops.fc2_dgrad_swiglu(dy, base.w2, seg, e, y1, row_prob, m=m,
+                                       a_rows=rows, tl=g2, l2=adp, proj=proj, proj_split=split,
+                                       w2_kn=True)
         if proj is not None:         # g1 = dy1 [[s_g B_g, 0], [0, s_u B_u]]^T from the epilogue
             dy1, dp_part, part = out
             g1 = ops.sum_parts(part, seg)
@@ -330,9 +339,11 @@ class _MoELoRALayerFn(torch.autograd.Function):
         if base.act_fp8:
             dy1q, dy1s = ops.quantize_rows_fp8(dy1, seg=seg, col_scale=base.w1_scale, m=m)
             dx_perm = ops.grouped_gemm(dy1q, base.w1t, seg, e, m=m, tl=g1, l=a1cat, a_scale=dy1s)
-        else:
+        elif base.fp8:
             dx_perm = ops.grouped_gemm(dy1, base.w1t, seg, e, m=m, tl=g1, l=a1cat,
                                        b_scale=base.w1_scale, scale_per_k=True)
+        else:   # W1 [E, 2F, H] read k-major: dx = dy1 @ W1[e]
+            dx_perm = ops.grouped_gemm(dy1, base.w1, seg, e, m=m, tl=g1, l=a1cat, b_kn=True)
         # router: softmax backward over the k selected logits
         dl, dlogits = ops.router_backward(dp_part, dest, w, idx, e,
                                           dense=ctx.logits_supplied and ctx.needs_input_grad[1])

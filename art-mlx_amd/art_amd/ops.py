@@ -230,14 +230,17 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
                  tl: torch.Tensor | None = None, l: torch.Tensor | None = None,
                  alpha: float = 1.0, out_fp32: bool = False,
                  out: torch.Tensor | None = None, b_scale: torch.Tensor | None = None,
-                 scale_per_k: bool = False, a_scale: torch.Tensor | None = None) -> torch.Tensor:
+                 scale_per_k: bool = False, a_scale: torch.Tensor | None = None,
+                 b_kn: bool = False) -> torch.Tensor:
     """C = alpha * (A[row(m)] @ B[e]^T + Tl @ L[e]^T) per expert segment.
 
     a [*, K] bf16; b [E, N, K] bf16 (last dim contiguous), or fp8 e4m3fn with
     ``b_scale`` [E, N] (per row) / [E, K] (``scale_per_k``): B = bf16(q * s);
     tl [M, kt], l [E, N, kt].  W8A8: ``a`` fp8 e4m3fn with ``a_scale`` per A
     source row (``quantize_rows_fp8``), fp8 ``b`` with optional per-row
-    ``b_scale``; the fp8 MFMA computes s_a s_b (A_q B_q^T).
+    ``b_scale``; the fp8 MFMA computes s_a s_b (A_q B_q^T).  ``b_kn``: b is
+    bf16 [E, K, N] (k-major, e.g. a forward weight read by its data
+    gradient) and C = alpha * (A @ b[e] + Tl @ L[e]^T).
     """
     _cuda(a, b, seg, a_rows, tl, l, b_scale, a_scale)
     f16 = a.dtype == torch.float16
@@ -247,10 +250,15 @@ def grouped_gemm(a: torch.Tensor, b: torch.Tensor, seg: torch.Tensor, num_expert
         _need(b.dtype == torch.float16 and b_scale is None and a_scale is None,
               "fp16 A needs fp16 B and no scales")
         fmt, bsc, bs_es = _lib.F16, None, 0
+    elif b_kn:
+        _need(b.dtype == torch.bfloat16 and b_scale is None and a_scale is None,
+              "k-major B must be bf16 (no scales)")
+        fmt, bsc, bs_es = _lib.B_KN, None, 0
     else:
         fmt, bsc, bs_es = _weight_format(b, b_scale, scale_per_k, a_scale)
-    _need(b.dim() == 3 and b.shape[0] == num_experts, "B must be [E, N, K]")
-    n, k = b.shape[1], b.shape[2]
+    _need(b.dim() == 3 and b.shape[0] == num_experts, "B must be [E, N, K]" if not b_kn
+          else "B must be [E, K, N]")
+    n, k = (b.shape[2], b.shape[1]) if b_kn else (b.shape[1], b.shape[2])
     _need(a.shape[-1] == k, f"A has K={a.shape[-1]}, B has K={k}")
     if m is None:
         m = a_rows.shape[0] if a_rows is not None else a.shape[0]
@@ -346,7 +354,7 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
                      a_rows: torch.Tensor | None = None, tl: torch.Tensor | None = None,
                      l2: torch.Tensor | None = None, w2_scale: torch.Tensor | None = None,
                      a_scale: torch.Tensor | None = None, proj: torch.Tensor | None = None,
-                     proj_split: int = 0):
+                     proj_split: int = 0, w2_kn: bool = False):
     """(dy1 [M,2F] bf16, dp_part [n_parts, M] fp32) of the FC2 dgrad + SwiGLU backward.
     With ``proj`` [E, R, 2F] (the FC1 adapter's scaled B, rank padded to 16)
     the epilogue also projects dy1: returns (dy1, dp_part, part), ``part`` the
@@ -357,9 +365,15 @@ def fc2_dgrad_swiglu(a: torch.Tensor, w2t: torch.Tensor, seg: torch.Tensor, num_
     W8A8 (``a_scale``): ``a`` is fp8 with the FC2 row scales already folded in
     (``quantize_rows_fp8(..., col_scale=w2_scale)``) and ``w2_scale`` is None."""
     _cuda(a, w2t, seg, y1, row_prob, a_rows, tl, l2, w2_scale, a_scale, proj)
-    e, f, k = w2t.shape
-    _need(w2t.is_contiguous(), "w2t must be contiguous [E, F, K]")
-    fmt, wsc, _ = _weight_format(w2t, w2_scale, True, a_scale)
+    if w2_kn:   # the FC2 weight itself, [E, K, F] (no transposed copy)
+        e, k, f = w2t.shape
+        _need(w2t.is_contiguous() and w2t.dtype == torch.bfloat16 and w2_scale is None
+              and a_scale is None, "k-major W2 must be contiguous bf16 [E, K, F]")
+        fmt, wsc = _lib.B_KN, None
+    else:
+        e, f, k = w2t.shape
+        _need(w2t.is_contiguous(), "w2t must be contiguous [E, F, K]")
+        fmt, wsc, _ = _weight_format(w2t, w2_scale, True, a_scale)
     _need(y1.is_contiguous() and y1.shape == (m, 2 * f), "y1 must be contiguous [M, 2F]")
     kt = 0
     ldt = 0

@@ -200,9 +200,40 @@ __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, c
   }
 }
 
-// MFMA operands of one 16-wide k step from a swizzled stage (rows of BK bf16).
-// Row blocks i >= tmv (no valid row) are not read.
-template <int TM, int TN, int WTM, int WTN, int A_BYTES, int BK = 64>
+// k-major B stages (the weight in its forward layout, [K][N] per expert):
+// the stage holds BK rows of k, each BN columns of n (BN * 2 bytes), and the
+// 16-byte chunk c of row k sits at physical chunk c ^ ((k & 3) << 2).  The
+// MFMA B operand wants 8 consecutive k of one column per lane; gfx950's
+// transposing LDS read delivers them: within a 16-lane group, lane s names 4
+// columns (8 bytes) of row s / 4 and lane i receives column i of those 4 rows.
+// Two reads (rows k0 .. k0+3 and k0+4 .. k0+7) make one fragment; lane l's
+// group covers columns 16 ((l / 16) & 1) .. +15 of the 32-column block and
+// k0 = 16 kk + 8 (l / 32), the 32x32x16 operand layout.  The row XOR spreads
+// the 4 rows x 32 bytes of a 16-lane read (and the 4 x 64 of a 32-lane pass)
+// over distinct banks.
+typedef short kn_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) kn_v4i16 *kn_lds_v4;
+
+template <int BN>
+__device__ __forceinline__ bf16x8 kn_frag(const char *stb, int kk, int col0, int lrow, int lk) {
+  const int s = lrow & 15;
+  const int col = col0 + 16 * (lrow >> 4) + 4 * (s & 3);
+  const int r = kk * 16 + 8 * lk + (s >> 2);              // r & 3 == s >> 2 (r % 8 < 4)
+  const int off = (((col >> 3) ^ ((s >> 2) << 2)) << 4) + ((col & 7) << 1);
+  const char *p = stb + r * (2 * BN) + off;
+  kn_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((kn_lds_v4)p);
+  kn_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((kn_lds_v4)(p + 4 * (2 * BN)));
+  bf16x8 v;
+  __builtin_memcpy(&v, &lo, 8);
+  __builtin_memcpy((char *)&v + 8, &hi, 8);
+  return v;
+}
+
+// MFMA operands of one 16-wide k step from a swizzled stage (rows of BK bf16;
+// with BKN, B in the k-major layout above).  Row blocks i >= tmv (no valid
+// row) are not read.
+template <int TM, int TN, int WTM, int WTN, int A_BYTES, int BK = 64, bool BKN = false,
+          int BN = 0>
 __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int wn, int lrow, int lk,
                                            bf16x8 (&af)[TM], bf16x8 (&bfv)[TN], int tmv = TM) {
 #pragma unroll
@@ -213,9 +244,43 @@ __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int w
   }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int r = wn * WTN + j * 32 + lrow;
-    bfv[j] = *(const bf16x8 *)(st + A_BYTES + r * (2 * BK) +
-                               (((kk * 2 + lk) ^ chunk_swz<BK>(r)) << 4));
+    if constexpr (BKN) {
+      bfv[j] = kn_frag<BN>(st + A_BYTES, kk, wn * WTN + j * 32, lrow, lk);
+    } else {
+      const int r = wn * WTN + j * 32 + lrow;
+      bfv[j] = *(const bf16x8 *)(st + A_BYTES + r * (2 * BK) +
+                                 (((kk * 2 + lk) ^ chunk_swz<BK>(r)) << 4));
+    }
+  }
+}
+
+// Stage DMA with a k-major B: A as in issue_stage (shift sh_a), B rows of k at
+// boff[i] + sh_b (sh_b: the stage's first k row); past the last k-tile
+// (partial, klim < kb + BK) rows clamp to klim - 1 (never multiplied).
+template <int A_PW, int B_PW, int A_BYTES, int BN, bool PARTIAL>
+__device__ __forceinline__ void issue_stage_kn(char *st, int wave, int lane, const char *abase,
+                                               const char *bbase, const uint32_t (&aoff)[A_PW],
+                                               const uint32_t (&boff)[B_PW], int kb, int klim,
+                                               uint32_t ldb2, int a_blocks) {
+  constexpr int RPK = 64 / (BN / 8);                       // k rows per 1 KB block
+  constexpr int CPR = 8, RPB = 8;                          // A: 64-wide k-tiles
+#pragma unroll
+  for (int i = 0; i < A_PW; ++i) {
+    const int bi = wave * A_PW + i;
+    if (bi >= a_blocks) continue;
+    int off = kb;                      // a partial k-tile re-reads the row's last chunk
+    if (PARTIAL) {
+      const int ch = (lane % CPR) ^ chunk_swz<64>(bi * RPB + lane / CPR);
+      off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
+    }
+    dma16((const bf16 *)(abase + (aoff[i] + (uint32_t)(off * 2))), st + bi * 1024);
+  }
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int kr = (wave * B_PW + i) * RPK + lane / (BN / 8);
+    const int row = kb + kr < klim ? kb : klim - 1 - kr;    // row offset beyond kr
+    dma16((const bf16 *)(bbase + (boff[i] + (uint32_t)row * ldb2)),
+          st + A_BYTES + (wave * B_PW + i) * 1024);
   }
 }
 
@@ -223,7 +288,7 @@ __device__ __forceinline__ void load_frags(const char *st, int kk, int wm, int w
 // moved in 1 KB DMA blocks of 16 rows; 16-byte chunk c of row r lives at
 // physical chunk c ^ swz8(r).
 enum { B_BF16 = ART_MOE_B_BF16, B_FP8_ROWSCALE = ART_MOE_B_FP8_ROWSCALE,
-       B_FP8_KSCALE = ART_MOE_B_FP8_KSCALE, B_FP8_AB = ART_MOE_AB_FP8 };
+       B_FP8_KSCALE = ART_MOE_B_FP8_KSCALE, B_FP8_AB = ART_MOE_AB_FP8, B_KN = ART_MOE_B_KN };
 
 __device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
@@ -502,6 +567,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr bool W8 = BQ8 == B_FP8_ROWSCALE || BQ8 == B_FP8_KSCALE;  // fp8 B, bf16 A
   constexpr bool A8 = BQ8 == B_FP8_AB;                               // fp8 A and B
+  constexpr bool BKN = BQ8 == B_KN;   // bf16 B stored k-major ([K][N]: the forward weight)
   constexpr int KPS = A8 ? 2 * BK : BK;  // base-product k per stage (64-byte rows: 64 fp8)
   constexpr int CPR = BK / 8, RPB = 64 / CPR;  // 16-byte chunks per row, rows per 1 KB block
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
@@ -536,6 +602,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   static_assert(EPI2_NH >= 1, "SwiGLU backward staging (dg and du of a row group) must fit the LDS ring");
   static_assert(!W8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
   static_assert(!F16 || (EPI == EPI_STORE && BQ8 == B_BF16), "fp16 operands: plain store products");
+  static_assert(!BKN || (BK == 64 && BN >= 128 && EPI != EPI_SWIGLU_FWD),
+                "k-major B: 64-wide k-tiles, BN >= 128, data-gradient products");
 
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES + PJ_BYTES];
   float *sRed = (float *)(smem + LDS_BYTES);
@@ -617,6 +685,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
     // 32-bit byte offsets from wave-uniform bases (the host checks that every
     // operand spans less than 4 GiB).
     const char *abase = (const char *)p.a;
+    const uint32_t ldb2 = (uint32_t)p.ldb * 2u;   // k-major B: bytes per k row
     const char *bbase = (W8 || A8) ? (const char *)p.b + (int64_t)e * p.b_es
                                    : (const char *)(p.b + (int64_t)e * p.b_es);
     uint32_t aoff[A_PW], boff[W8 ? B_PW8 : B_PW];
@@ -635,6 +704,17 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         const int n = b_source_row<EPI, BN>(r, nt, p.N, p.F);
         const uint32_t ch = (uint32_t)((lane & 3) ^ swz8(r));
         boff[i] = (uint32_t)n * (uint32_t)p.ldb + ch * 16u;
+      }
+    } else if constexpr (BKN) {
+      // k row kr of the stage (per 1 KB block), physical chunk lane % (BN/8)
+      // holding columns nt*BN + 8 c (clamped into N; never multiplied past it)
+#pragma unroll
+      for (int i = 0; i < B_PW; ++i) {
+        const int kr = (wave * B_PW + i) * (64 / (BN / 8)) + lane / (BN / 8);
+        const int c = (lane % (BN / 8)) ^ ((kr & 3) << 2);
+        int n = nt * BN + c * 8;
+        n = n < p.N - 8 ? n : p.N - 8;
+        boff[i] = ((uint32_t)kr * (uint32_t)p.ldb + (uint32_t)n) * 2u;
       }
     } else {
 #pragma unroll
@@ -700,12 +780,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         if (BQ8 == B_FP8_KSCALE && wave == 0 && lane < BK / 4)                                \
           dma16v(p.b_scale + (int64_t)e * p.bs_es + (ks) * BK + lane * 4,                     \
                  st_ + A_BYTES + B_BYTES);                                                    \
+      } else if constexpr (BKN) {                                                             \
+        issue_stage_kn<A_PW, B_PW, A_BYTES, BN, false>(st_, wave, lane, abase, bbase, aoff,   \
+                                                       boff, (ks) * BK, p.K, ldb2, a_blocks); \
       } else {                                                                                \
         issue_stage<A_PW, B_PW, A_BYTES>(st_, wave, abase, bbase, aoff, boff,                 \
                                          (uint32_t)((ks) * BK * 2), a_blocks);                \
       }                                                                                       \
     } else if ((ks) < nk_main) {                                                              \
-      if constexpr (BQ8 == B_BF16)                                                            \
+      if constexpr (BKN)                                                                      \
+        issue_stage_kn<A_PW, B_PW, A_BYTES, BN, true>(st_, wave, lane, abase, bbase, aoff,    \
+                                                      boff, (ks) * BK, p.K, ldb2, a_blocks);  \
+      else if constexpr (BQ8 == B_BF16)                                                       \
         issue_stage_tail<A_PW, B_PW, A_BYTES, BK>(st_, wave, lane, abase, bbase, aoff, boff,  \
                                                   (ks) * BK, p.K, a_blocks);                  \
     } else {                                                                                  \
@@ -838,18 +924,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         ART_FENCE();
         load_frags8<TM, TN, WTM, WTN, A_BYTES, BQ8>(st, 3, wm, wn, lrow, lk, af1, bf1, bsc, ksc, tmv);
       } else {
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 0, wm, wn, lrow, lk, af0, bf0, tmv);
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 1, wm, wn, lrow, lk, af1, bf1, tmv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK, BKN, BN>(st, 0, wm, wn, lrow, lk, af0, bf0, tmv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK, BKN, BN>(st, 1, wm, wn, lrow, lk, af1, bf1, tmv);
         ART_FENCE();
         mma_step<TM, TN, F16>(acc, af0, bf0, tmv);
         ART_FENCE();
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 2, wm, wn, lrow, lk, af0, bf0, tmv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK, BKN, BN>(st, 2, wm, wn, lrow, lk, af0, bf0, tmv);
         ART_FENCE();
         mma_step<TM, TN, F16>(acc, af1, bf1, tmv);
         ART_FENCE();
         if (late_issue && ks + STAGES - 1 < nk) ART_ISSUE(ks + STAGES - 1);
         ART_FENCE();
-        load_frags<TM, TN, WTM, WTN, A_BYTES>(st, 3, wm, wn, lrow, lk, af1, bf1, tmv);
+        load_frags<TM, TN, WTM, WTN, A_BYTES, BK, BKN, BN>(st, 3, wm, wn, lrow, lk, af1, bf1, tmv);
       }
       ART_FENCE();
       mma_step<TM, TN, F16>(acc, af0, bf0, tmv);
@@ -869,7 +955,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       const int nkk = (klim - kb) >= BK ? BK / 16 : (klim - kb) / 16;
       for (int kk = 0; kk < nkk; ++kk) {
         bf16x8 af[TM], bfv[TN];
-        load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, kk, wm, wn, lrow, lk, af, bfv, tmv);
+        if (BKN && main)   // k-major base stage; the LoRA stages are row-major
+          load_frags<TM, TN, WTM, WTN, A_BYTES, BK, BKN, BN>(st, kk, wm, wn, lrow, lk, af, bfv, tmv);
+        else
+          load_frags<TM, TN, WTM, WTN, A_BYTES, BK>(st, kk, wm, wn, lrow, lk, af, bfv, tmv);
         if (A8) {  // LoRA terms join the fp8 accumulators pre-divided by the row scales
 #pragma unroll
           for (int i = 0; i < TM; ++i) af[i] = scale_frag(af[i], 1.0f / asc[i]);
@@ -1210,6 +1299,25 @@ static int launch_fp8(int fmt, const NTArgs &p, const int32_t *seg, int64_t M, h
   return launch_nt<256, 256, 2, 4, 2, EPI, B_FP8_KSCALE>(p, seg, M, s, what);
 }
 
+// k-major-B products (data gradients on the forward weight layout): the
+// macro tiles with 64-wide k-tiles and BN >= 128; others fall back to 5 / 3.
+template <int EPI>
+static int launch_kn(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
+                     const char *what) {
+  switch (cfg) {
+    case 0: return launch_nt<128, 128, 2, 2, 4, EPI, B_KN>(p, seg, M, s, what);
+    case 3: return launch_nt<128, 256, 2, 4, 3, EPI, B_KN>(p, seg, M, s, what);
+    case 5: return launch_nt<256, 256, 2, 4, 2, EPI, B_KN>(p, seg, M, s, what);
+    case 6: return launch_nt<256, 256, 4, 2, 2, EPI, B_KN>(p, seg, M, s, what);
+    case 11: return launch_nt<128, 256, 2, 4, 2, EPI, B_KN>(p, seg, M, s, what);
+    default:
+      if constexpr (EPI == EPI_SWIGLU_BWD)
+        return launch_nt<128, 256, 2, 4, 3, EPI, B_KN>(p, seg, M, s, what);
+      else
+        return launch_nt<256, 256, 2, 4, 2, EPI, B_KN>(p, seg, M, s, what);
+  }
+}
+
 // Macro tile of one product: ART_MOE_GEMM_TILE_<which> (STORE, FC1 or BWD),
 // else ART_MOE_GEMM_TILE, else the default.
 static int tile_cfg(int dflt, const char *which) {
@@ -1232,9 +1340,16 @@ static int cfg_bn(int c) {
 
 // Output columns per column tile of the SwiGLU products: FC1 tiles cover BN/2
 // columns of h, the FC2 data gradient BN columns of dg (and of du).
+static int kn_cfg(int c) {  // the macro tile launch_kn runs for config c
+  return (c == 0 || c == 3 || c == 5 || c == 6 || c == 11) ? c : -1;
+}
 static int swiglu_tile_cols(int product, int32_t fmt) {
   if (product == 0)
     return (fmt == ART_MOE_B_BF16 ? cfg_bn(tile_cfg(kTileSwigluFwd, "FC1")) : 256) / 2;
+  if (fmt == ART_MOE_B_KN) {
+    const int c = kn_cfg(tile_cfg(kTileSwigluBwd, "BWD"));
+    return c < 0 ? 256 : cfg_bn(c);
+  }
   return fmt == ART_MOE_B_BF16 ? cfg_bn(tile_cfg(kTileSwigluBwd, "BWD")) : 256;
 }
 
@@ -1308,15 +1423,16 @@ static int set_projection(NTArgs &p, const void *pj_b, int64_t pj_es, int32_t pj
 static int check_common(const void *a, int64_t lda, const void *b, int64_t ldb,
                         const int32_t *seg, int32_t E, int64_t M, int32_t K, int32_t kt,
                         const void *tl, int64_t ldt, const void *l, int64_t ldl,
-                        const char *who) {
+                        const char *who, int64_t ldb_min = -1) {
+  if (ldb_min < 0) ldb_min = K;   // row-major B [N][K]; k-major B [K][N] passes N
   ART_REQUIRE(E >= 1 && E <= 1024, "%s: need 1 <= E <= 1024 (E=%d)", who, E);
   ART_REQUIRE(M >= 0 && M < INT32_MAX, "%s: M out of range", who);
   ART_REQUIRE(K > 0 && K % 16 == 0, "%s: K must be a positive multiple of 16 (K=%d)", who, K);
   ART_REQUIRE(kt >= 0 && kt % 16 == 0, "%s: LoRA kt must be a multiple of 16 (kt=%d)", who, kt);
   ART_REQUIRE((a || M == 0) && b && seg, "%s: null pointer", who);  // no rows: A is never read
-  ART_REQUIRE(lda >= K && lda % 8 == 0 && ldb >= K && ldb % 8 == 0,
-              "%s: leading dimensions must be >= K and multiples of 8 (lda=%lld ldb=%lld)", who,
-              (long long)lda, (long long)ldb);
+  ART_REQUIRE(lda >= K && lda % 8 == 0 && ldb >= ldb_min && ldb % 8 == 0,
+              "%s: leading dimensions must be >= K (B: its row length) and multiples of 8 "
+              "(lda=%lld ldb=%lld)", who, (long long)lda, (long long)ldb);
   ART_REQUIRE(aligned16(a) && aligned16(b), "%s: A and B must be 16-byte aligned", who);
   // The kernels address operand rows with 32-bit byte offsets.
   const double k4g = 4294967296.0;
@@ -1339,7 +1455,7 @@ static int check_fp8(int32_t fmt, const void *b, int64_t ldb, const float *b_sca
                      int64_t bs_es, int32_t K, int32_t N, int64_t lda, const float *a_scale,
                      const char *who) {
   ART_REQUIRE(fmt == ART_MOE_B_BF16 || fmt == ART_MOE_B_FP8_ROWSCALE ||
-                  fmt == ART_MOE_B_FP8_KSCALE || fmt == ART_MOE_AB_FP8,
+                  fmt == ART_MOE_B_FP8_KSCALE || fmt == ART_MOE_AB_FP8 || fmt == ART_MOE_B_KN,
               "%s: unknown weight format %d", who, fmt);  // (ART_MOE_F16: grouped_gemm only)
   if (fmt == ART_MOE_AB_FP8) {
     ART_REQUIRE(K % 64 == 0, "%s: fp8 operands need K a multiple of 64 (K=%d)", who, K);
@@ -1350,6 +1466,12 @@ static int check_fp8(int32_t fmt, const void *b, int64_t ldb, const float *b_sca
     return ART_MOE_OK;
   }
   ART_REQUIRE(!a_scale, "%s: A row scales need fp8 A (ART_MOE_AB_FP8)", who);
+  if (fmt == ART_MOE_B_KN) {
+    ART_REQUIRE(!b_scale, "%s: k-major bf16 weights take no scales", who);
+    ART_REQUIRE(ldb >= N && N >= 8, "%s: k-major weights need ldb >= N >= 8 (ldb=%lld N=%d)", who,
+                (long long)ldb, N);
+    return ART_MOE_OK;
+  }
   if (fmt == ART_MOE_B_BF16) return ART_MOE_OK;
   ART_REQUIRE(K % 64 == 0, "%s: fp8 weights need K a multiple of 64 (K=%d)", who, K);
   ART_REQUIRE(ldb % 16 == 0, "%s: fp8 weights need ldb a multiple of 16", who);
@@ -1369,7 +1491,8 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
                                     int64_t M, int32_t N, int32_t K, float alpha, void *c,
                                     int64_t ldc, int32_t c_fp32, void *stream) {
   clear_error();
-  int rc = check_common(a, lda, b, ldb, seg, E, M, K, kt, tl, ldt, l, ldl, "grouped_gemm");
+  int rc = check_common(a, lda, b, ldb, seg, E, M, K, kt, tl, ldt, l, ldl, "grouped_gemm",
+                        b_format == ART_MOE_B_KN ? (int64_t)N : (int64_t)K);
   if (rc) return rc;
   const bool f16 = b_format == ART_MOE_F16;
   if (f16) {
@@ -1382,8 +1505,11 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
               "grouped_gemm: need N a positive multiple of 8 and an output");
   ART_REQUIRE(ldc >= N && ldc % 8 == 0 && aligned16(c),
               "grouped_gemm: C needs ldc >= N, ldc %% 8 == 0 and 16-byte alignment");
-  ART_REQUIRE((double)N * (double)(ldb > ldl ? ldb : ldl) * 2.0 < 4294967296.0,
+  ART_REQUIRE((double)(b_format == ART_MOE_B_KN ? K : N) * (double)ldb * 2.0 < 4294967296.0 &&
+                  (double)N * (double)ldl * 2.0 < 4294967296.0,
               "grouped_gemm: one expert's B / L must span less than 4 GiB");
+  ART_REQUIRE(b_format != ART_MOE_B_KN || b_estride >= (int64_t)K * ldb,
+              "grouped_gemm: k-major B needs b_estride >= K * ldb");
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows; p.a_scale = a_scale;
@@ -1399,6 +1525,8 @@ extern "C" int art_moe_grouped_gemm(const void *a, int64_t lda, const int32_t *a
     if (N <= 128) return launch_nt<128, 128, 2, 2, 4, EPI_STORE, B_BF16, 64, true>(p, seg, M, s, "grouped_gemm/f16/n128");
     return launch_nt<256, 256, 2, 4, 2, EPI_STORE, B_BF16, 64, true>(p, seg, M, s, "grouped_gemm/f16");
   }
+  if (b_format == ART_MOE_B_KN)
+    return launch_kn<EPI_STORE>(tile_cfg(kTileStore, "STORE"), p, seg, M, s, "grouped_gemm/kn");
   if (b_format != ART_MOE_B_BF16) return launch_fp8<EPI_STORE>(b_format, p, seg, M, s, "grouped_gemm/fp8");
   if (N <= 32) return launch_nt<128, 32, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n32");
   if (N <= 64) return launch_nt<128, 64, 4, 1, 4, EPI_STORE>(p, seg, M, s, "grouped_gemm/n64");
@@ -1452,12 +1580,14 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
                                         int32_t pj_n, int32_t pj_split, float *pj_part,
                                         int32_t pj_tiles, void *stream) {
   clear_error();
-  int rc = check_common(a, lda, w2t, K, seg, E, M, K, kt, tl, ldt, l2, kt, "fc2_dgrad_swiglu");
+  const bool kn = w2_format == ART_MOE_B_KN;   // W2 [E][K][F] (forward layout) for W2T
+  int rc = check_common(a, lda, w2t, kn ? F : K, seg, E, M, K, kt, tl, ldt, l2, kt,
+                        "fc2_dgrad_swiglu", kn ? F : K);
   if (rc) return rc;
   ART_REQUIRE(w2_format != ART_MOE_B_FP8_ROWSCALE,
               "fc2_dgrad_swiglu: fp8 W2^T takes per-k scales (the FC2 output channels)");
-  rc = check_fp8(w2_format, w2t, K, w2_scale, w2_format == ART_MOE_AB_FP8 ? F : K, K, F, lda,
-                 a_scale, "fc2_dgrad_swiglu");
+  rc = check_fp8(w2_format, w2t, kn ? F : K, w2_scale, w2_format == ART_MOE_AB_FP8 ? F : K, K, F,
+                 lda, a_scale, "fc2_dgrad_swiglu");
   if (rc) return rc;
   ART_REQUIRE(F > 0 && F % 8 == 0, "fc2_dgrad_swiglu: F must be a positive multiple of 8 (F=%d)", F);
   ART_REQUIRE((y1 && row_prob && dy1 && dp_part) || M == 0, "fc2_dgrad_swiglu: null pointer");
@@ -1465,7 +1595,7 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
   if (M == 0) return ART_MOE_OK;
   NTArgs p{};
   p.a = (const bf16 *)a; p.lda = lda; p.a_rows = a_rows; p.a_scale = a_scale;
-  p.b = (const bf16 *)w2t; p.ldb = K; p.b_es = (int64_t)F * K;
+  p.b = (const bf16 *)w2t; p.ldb = kn ? F : K; p.b_es = (int64_t)F * K;
   p.b_scale = w2_scale; p.bs_es = w2_format == ART_MOE_AB_FP8 ? F : K;
   p.t = kt ? (const bf16 *)tl : nullptr; p.ldt = ldt;
   p.l = kt ? (const bf16 *)l2 : nullptr; p.ldl = kt; p.l_es = (int64_t)F * kt; p.kt = kt;
@@ -1478,6 +1608,9 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
               "fc2_dgrad_swiglu: pj_split must be 0 or a multiple of 16 below pj_n (%d, %d)",
               pj_split, pj_n);
   p.pj_split = pj_b ? pj_split : 0;
+  if (kn)
+    return launch_kn<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwd, "BWD"), p, seg, M,
+                                     as_stream(stream), "fc2_dgrad_swiglu/kn");
   if (w2_format != ART_MOE_B_BF16)
     return launch_fp8<EPI_SWIGLU_BWD>(w2_format, p, seg, M, as_stream(stream),
                                       "fc2_dgrad_swiglu/fp8");

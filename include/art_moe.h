@@ -76,6 +76,11 @@ extern "C" {
  * fp16 MFMA, fp32 accumulation); the reference's grouped LoRA operators accept
  * fp16 as well as bf16 (cute_grouped_lora_quack.py:155-158). */
 #define ART_MOE_F16 4
+/* art_moe_grouped_gemm and art_moe_fc2_dgrad_swiglu: bf16 weights stored
+ * k-major, B [E][K][N] with row stride ldb >= N (b_estride >= K * ldb): the
+ * data-gradient products read W1 / W2 in their forward layout, so no
+ * transposed copy is kept.  Needs N >= 8, N % 8 == 0. */
+#define ART_MOE_B_KN 5
 #define ART_MOE_SEG_LEN(E) ((1 + ART_MOE_SEG_NBM) * ((E) + 1))
 
 /* Library version, e.g. 100 for 0.1.0. */

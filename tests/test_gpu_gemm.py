@@ -424,3 +424,74 @@ def test_fc2_dgrad_epilogue_projection(device, e, m, f, h, rp, tile, split, monk
     ref = _ref_grouped(dy1[:cut].float().cpu(), proj, counts)
     assert rel(gp[:cut], ref) < 1e-2
     assert torch.count_nonzero(gp[cut:]) == 0
+
+
+# ------------------------------------------------- k-major B (forward weight layout)
+@pytest.mark.parametrize("e,m,n,k,kt,gather,tile", [
+    (8, 1000, 2048, 1536, 32, False, None),   # FC1 data-gradient shape, default 256x256
+    (8, 1000, 768, 2048, 0, True, "3"),       # 128 x 256, 3 stages
+    (5, 700, 200, 1552, 16, True, None),      # N past the last column tile, partial k-tile
+    (4, 300, 136, 80, 0, False, "0"),         # 128 x 128, 4 stages
+    (6, 900, 512, 256, 0, False, "11"),
+])
+def test_grouped_gemm_k_major_b(device, e, m, n, k, kt, gather, tile, monkeypatch):
+    """B stored [E, K, N] (read through transposing LDS reads) gives the same
+    bits as the row-major kernel on B transposed (same tile, same k order),
+    and matches fp32 torch to the bf16 bar."""
+    if tile is not None:
+        monkeypatch.setenv("ART_MOE_GEMM_TILE_STORE", tile)
+    ops = _ops()
+    print(f"k-major B e={e} m={m} n={n} k={k} kt={kt} gather={gather} tile={tile}", flush=True)
+    g = torch.Generator().manual_seed(n + k)
+    counts = _counts(e, m, seed=k)
+    t_src = 611
+    src = torch.randn(t_src if gather else m, k, generator=g).to(torch.bfloat16)
+    rows = torch.randint(0, t_src, (m,), generator=g, dtype=torch.int32) if gather else None
+    bkn = (torch.randn(e, k, n, generator=g) * 0.05).to(torch.bfloat16)
+    tl = l = None
+    if kt:
+        tl = torch.randn(m, kt, generator=g).to(torch.bfloat16)
+        l = (torch.randn(e, n, kt, generator=g) * 0.1).to(torch.bfloat16)
+    seg = ops.segments_from_counts(counts, e, device)
+    kw = dict(m=m, a_rows=rows.to(device) if gather else None,
+              tl=tl.to(device) if kt else None, l=l.to(device) if kt else None, alpha=0.5)
+    got = ops.grouped_gemm(src.to(device), bkn.to(device), seg, e, b_kn=True, **kw)
+    same = ops.grouped_gemm(src.to(device), bkn.transpose(1, 2).contiguous().to(device), seg, e,
+                            **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, same)
+    a_f = (src[rows.long()] if gather else src).float()
+    ref = _ref_grouped(a_f, bkn.transpose(1, 2), counts, tl, l, alpha=0.5)
+    assert rel(got, ref) < 1e-2
+
+
+@pytest.mark.parametrize("f,h,tile,rp", [(512, 1024, None, 32), (200, 512, None, 0),
+                                         (768, 2048, "5", 16)])
+def test_fc2_dgrad_swiglu_k_major_w2(device, f, h, tile, rp, monkeypatch):
+    """The FC2 data gradient reading W2 [E, H, F] directly equals the kernel
+    on the transposed copy bit for bit (dy1, dp partials, LoRA projection)."""
+    if tile is not None:
+        monkeypatch.setenv("ART_MOE_GEMM_TILE_BWD", tile)
+    ops = _ops()
+    e, m, kt = 8, 1100, 16
+    print(f"fc2 dgrad k-major W2 f={f} h={h} tile={tile} rp={rp}", flush=True)
+    g = torch.Generator().manual_seed(f + h)
+    counts = _counts(e, m - 13, seed=f)
+    seg = ops.segments_from_counts(counts, e, device)
+    dy = torch.randn(m, h, generator=g).to(torch.bfloat16).to(device)
+    w2 = (torch.randn(e, h, f, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    y1 = torch.randn(m, 2 * f, generator=g).to(torch.bfloat16).to(device)
+    prob = torch.rand(m, generator=g).to(device)
+    tl = torch.randn(m, kt, generator=g).to(torch.bfloat16).to(device)
+    l2 = (torch.randn(e, f, kt, generator=g) * 0.1).to(torch.bfloat16).to(device)
+    kw = dict(m=m, tl=tl, l2=l2)
+    if rp:
+        kw["proj"] = (torch.randn(e, rp, 2 * f, generator=g) * 0.05).to(torch.bfloat16).to(device)
+    a = ops.fc2_dgrad_swiglu(dy, w2, seg, e, y1, prob, w2_kn=True, **kw)
+    b = ops.fc2_dgrad_swiglu(dy, w2.transpose(1, 2).contiguous(), seg, e, y1, prob, **kw)
+    torch.cuda.synchronize()
+    cut = sum(counts)          # rows past the segments are not written
+    assert torch.equal(a[0][:cut], b[0][:cut])              # dy1 [M, 2F]
+    assert torch.equal(a[1][:, :cut], b[1][:, :cut])        # dp partials [parts, M]
+    if rp:
+        assert torch.equal(a[2][:, :cut], b[2][:, :cut])    # projection partials [tiles, M, R]

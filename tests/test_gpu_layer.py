@@ -308,3 +308,27 @@ def test_layer_fused_main_grad_accumulation(device, cfg_name):
         assert first["d" + n] is None and first["added_" + n], n
         assert torch.equal(snap[n].to(torch.bfloat16).cpu(), plain["d" + n]), n
         assert torch.equal(mg[n], 2 * snap[n]), n
+
+
+def test_layer_without_weight_copies_is_bit_identical(device):
+    """FrozenExperts without the transposed W2 copy (the FC2 data gradient
+    reads W2 k-major, as the FC1 one always reads W1) gives the same bits as
+    the default layer: same tiles, same k order."""
+    from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
+    print("layer without weight copies", flush=True)
+    inp = _small("C1", 512)
+    outs = []
+    for copy in (True, False):
+        base = FrozenExperts.build(inp.w_r.to(device), inp.w1.to(device), inp.w2.to(device),
+                                   w2_copy=copy)
+        assert base.w1t is None and (base.w2t is None) == (not copy)
+        lora = {n: inp.lora[n].to(device).requires_grad_() for n in NAMES}
+        x = inp.x.to(device).requires_grad_()
+        s = inp.cfg.scale
+        y, idx, counts, status = moe_lora_layer(x, base, *(lora[n] for n in NAMES), k=inp.cfg.k,
+                                                scales=(s, s, s))
+        y.backward(inp.dy.to(device))
+        torch.cuda.synchronize()
+        outs.append([y.detach(), x.grad] + [lora[n].grad for n in NAMES])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
