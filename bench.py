@@ -204,6 +204,41 @@ def copy_calibration(mib: int, reps: int) -> None:
     print(json.dumps({"copy_calibration_bytes_per_launch": n * 2, "reps": reps}))
 
 
+def fc1_vs_library(reps: int) -> None:
+    """The dominant kernel beside the vendor library on the same M, N, K: our
+    FC1 (fc1_swiglu: gathered rows, C1's 128 experts with 512 rows each, LoRA
+    off) and hipBLASLt's dense NT GEMM through torch.matmul (one weight for
+    all rows).  ``reps`` launches of each, timed with HIP events; the
+    profiler's counter passes run this mode for the side-by-side summary."""
+    import torch
+    from art_amd import ops
+    dev = torch.device("cuda:0")
+    t, h, e, k, f = 8192, 2048, 128, 8, 768
+    m = t * k
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(t, h, device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(e, 2 * f, h, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    prob = torch.rand(m, device=dev, generator=g)
+    rows = torch.randint(0, t, (m,), device=dev, generator=g, dtype=torch.int32)
+    seg = ops.segments_from_counts([m // e] * e, e, dev)
+    a = torch.randn(m, h, device=dev, generator=g).to(torch.bfloat16)
+    bt = torch.randn(2 * f, h, device=dev, generator=g).to(torch.bfloat16)
+    out = {}
+    for name, fn in (("fc1_swiglu", lambda: ops.fc1_swiglu(x, w1, seg, e, prob, m=m, a_rows=rows)),
+                     ("hipblaslt_dense", lambda: torch.matmul(a, bt.t()))):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        out[name] = {"us": round(us, 1), "tflops": round(2 * m * 2 * f * h / us / 1e6, 1)}
+    print(json.dumps({"fc1_vs_library": out, "M": m, "N": 2 * f, "K": h, "reps": reps}))
+
+
 def measured_traffic(cfg_name: str):
     """HBM bytes per launch of the dominant kernel from the committed profile
     summary (two rocprofv3 --pmc passes), or None when not measured."""
@@ -230,9 +265,14 @@ def main():
                          "(opt-in mode with its own tolerance; default W8A16 keeps the bf16 bar)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (profiler counter calibration)")
+    ap.add_argument("--fc1-vs-library", type=int, default=0, metavar="REPS",
+                    help="only run FC1 and hipBLASLt's dense GEMM of the same shape REPS times each")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration, 3)
+        return
+    if args.fc1_vs_library:
+        fc1_vs_library(args.fc1_vs_library)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
