@@ -42,8 +42,14 @@ from .kernels.grouped_lora_hip import padded_rank
 
 # The LoRA projections of h (forward) and dy1 (backward) run inside the
 # epilogues that produce h and dy1 (fp32 partials per column tile, then one
-# fixed-order sum); ART_MOE_FUSE_PROJ=0 runs them as separate narrow products.
+# fixed-order sum) when the projection is narrow: up to 16 padded rank
+# columns for h A_d, up to 32 for dy1 [B_g | B_u]^T (block-diagonal: 16 per
+# half).  Wider ones cost the epilogues more than the separate narrow products
+# they replace (measured: +0.4 ms per C3 step at ranks 64, +0.1-0.2 ms per C4
+# step for h A_d at rank 32), so they stay separate; ART_MOE_FUSE_PROJ=0
+# keeps all of them separate.
 FUSE_PROJECTIONS = os.environ.get("ART_MOE_FUSE_PROJ", "1") != "0"
+FUSE_MAX_WIDTH_FWD, FUSE_MAX_WIDTH_BWD = 16, 32
 
 
 @dataclass
@@ -248,7 +254,7 @@ class _MoELoRALayerFn(torch.autograd.Function):
         m = t * k
         rows = plan.row_token
         t1 = ops.grouped_gemm(x, a1p, plan.seg, e, m=m, a_rows=rows)
-        proj = a2p if FUSE_PROJECTIONS else None
+        proj = a2p if FUSE_PROJECTIONS and rpd <= FUSE_MAX_WIDTH_FWD else None
         if base.act_fp8:   # W8A8: x per token, h per routed row, scales in the epilogues
             xq, xs = ops.quantize_rows_fp8(x)
             out = ops.fc1_swiglu(xq, base.w1, plan.seg, e, plan.row_prob, m=m, a_rows=rows,
@@ -313,7 +319,7 @@ class _MoELoRALayerFn(torch.autograd.Function):
         ops.pack(*items)
         # FC2 data gradient with the SwiGLU backward in its epilogue
         g2 = ops.grouped_gemm(dy, bdp, seg, e, m=m, a_rows=rows, alpha=sd)
-        proj = gb if FUSE_PROJECTIONS else None
+        proj = gb if FUSE_PROJECTIONS and rpg + rpu <= FUSE_MAX_WIDTH_BWD else None
         split = 0 if fused_gu else rpg     # the dual adapter's gb is block-diagonal
         if base.act_fp8:
             # W8A8: the weights' per-k scales (the FC2 / FC1 output channels)

@@ -239,6 +239,28 @@ def fc1_vs_library(reps: int) -> None:
     print(json.dumps({"fc1_vs_library": out, "M": m, "N": 2 * f, "K": h, "reps": reps}))
 
 
+def other_configs(steps: int = 5, warmup: int = 2) -> dict:
+    """The other workloads at full size, briefly (after the C1 line's own
+    timing): ms per layer step, tokens/s and FC1's fraction of the bf16 peak,
+    so that C2 (Zipf replay), C3 (T = 32768, router LoRA, fp32 main_grad) and
+    C4 (fp8 weights) are measured in the same run."""
+    import torch
+    from art_amd.workloads import CONFIGS
+    out = {}
+    for name in ("C2", "C3", "C4"):
+        cfg = CONFIGS[name]
+        ms, (tf, cf), _ = gpu_bench(cfg, steps, warmup)
+        m, h, f, r = cfg.M, cfg.H, cfg.F, cfg.r
+        fl = 2 * m * h * 2 * f + 2 * m * 2 * f * r + 2 * m * f * r
+        fc1_ms = tf["fc1_swiglu"] / max(cf["fc1_swiglu"], 1)
+        out[name] = {"workload": cfg.note, "T": cfg.T, "ms_per_step": round(ms, 4),
+                     "tokens_per_s": round(cfg.T / (ms / 1e3), 1),
+                     "fc1_frac_of_bf16_peak": round(fl / (fc1_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "steps": steps, "warmup": warmup}
+        torch.cuda.empty_cache()
+    return out
+
+
 def measured_traffic(cfg_name: str):
     """HBM bytes per launch of the dominant kernel from the committed profile
     summary (two rocprofv3 --pmc passes), or None when not measured."""
@@ -265,6 +287,8 @@ def main():
                          "(opt-in mode with its own tolerance; default W8A16 keeps the bf16 bar)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (profiler counter calibration)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="C1 run: skip the short C2 / C3 / C4 measurements added to the line")
     ap.add_argument("--fc1-vs-library", type=int, default=0, metavar="REPS",
                     help="only run FC1 and hipBLASLt's dense GEMM of the same shape REPS times each")
     args = ap.parse_args()
@@ -344,6 +368,8 @@ def main():
         "dispatch_combine_gbs": round(comb_bytes / (disp_ms * 1e-3) / 1e9, 1) if disp_ms else None,
         "kernels_ms_per_step": kernels,
     }
+    if args.config == "C1" and not args.no_other_configs:
+        result["other_configs"] = other_configs()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_tokens, args.cpu_iters)
         result["cpu_baseline"]["gpu_over_cpu"] = round(tokens_per_s / result["cpu_baseline"]["value"], 1)
