@@ -90,8 +90,41 @@ struct NTArgs {
 
 typedef __attribute__((address_space(3))) void *lds_void_ptr;
 
-__device__ __forceinline__ void dma16(const bf16 *g, void *lds) {
-  __builtin_amdgcn_global_load_lds((const void *)g, (lds_void_ptr)lds, 16, 0, 0);
+// Global -> LDS DMA, 16 bytes per lane: lane i fills bytes 16 i .. 16 i + 15 of
+// the wave-uniform LDS address lds (through M0) from sbase + voff (sbase
+// wave-uniform, voff per lane).
+//
+// ASM: issued as inline asm, so that the compiler's wait model does not see an
+// LDS write in flight (every wait for these loads is explicit anyway:
+// wait_stages and the barriers).  Kernels that read B with transposing LDS
+// reads use it: for those reads the compiler otherwise waits for every
+// outstanding DMA (vmcnt(0)), including the next stage's, just issued.  The
+// other kernels keep the builtin, which schedules better around the DMA.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  // the low 32 bits of a flat address inside the LDS aperture are the LDS offset
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+// A wave-uniform pointer in scalar registers (the callers' bases are uniform;
+// this states it where the compiler cannot prove it).
+__device__ __forceinline__ const char *uniform_ptr(const void *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const char *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+template <bool ASM>
+__device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, void *lds) {
+  if constexpr (ASM) {
+    uint32_t m0_save;   // M0 is reserved by the compiler: restored after the load
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(m0_save)
+        : "v"(voff), "s"(uniform_ptr(sbase)), "s"(lds_addr(lds))
+        : "memory");
+  } else {
+    __builtin_amdgcn_global_load_lds((const void *)(sbase + voff), (lds_void_ptr)lds, 16, 0, 0);
+  }
 }
 
 template <int N>
@@ -144,7 +177,7 @@ __device__ __forceinline__ int chunk_swz(int r) {
 // One stage of operand DMA for this wave: A_PW blocks of A rows, B_PW of B rows.
 // A blocks whose first row is >= a_blocks * RPB (past the tile's valid rows)
 // are skipped when a_blocks says so (callers pass a huge value otherwise).
-template <int A_PW, int B_PW, int A_BYTES>
+template <int A_PW, int B_PW, int A_BYTES, bool DA = false>
 __device__ __forceinline__ void issue_stage(char *st, int wave, const char *abase,
                                             const char *bbase, const uint32_t (&aoff)[A_PW],
                                             const uint32_t (&boff)[B_PW], uint32_t sh,
@@ -152,10 +185,10 @@ __device__ __forceinline__ void issue_stage(char *st, int wave, const char *abas
 #pragma unroll
   for (int i = 0; i < A_PW; ++i)
     if (wave * A_PW + i < a_blocks)
-      dma16((const bf16 *)(abase + (aoff[i] + sh)), st + (wave * A_PW + i) * 1024);
+      dma16<DA>(abase, aoff[i] + sh, st + (wave * A_PW + i) * 1024);
 #pragma unroll
   for (int i = 0; i < B_PW; ++i)
-    dma16((const bf16 *)(bbase + (boff[i] + sh)), st + A_BYTES + (wave * B_PW + i) * 1024);
+    dma16<DA>(bbase, boff[i] + sh, st + A_BYTES + (wave * B_PW + i) * 1024);
 }
 
 // Weight row feeding tile-local B row r of column tile nt (clamped into range).
@@ -177,7 +210,7 @@ __device__ __forceinline__ int b_source_row(int r, int nt, int N, int F) {
 // chunk (those columns are never multiplied).  A 1 KB block holds RPB rows of
 // CPR chunks; the logical chunk of block b's slot is
 // (lane % CPR) ^ chunk_swz(RPB b + lane / CPR).
-template <int A_PW, int B_PW, int A_BYTES, int BK = 64>
+template <int A_PW, int B_PW, int A_BYTES, int BK = 64, bool DA = false>
 __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, const char *abase,
                                                  const char *bbase, const uint32_t (&aoff)[A_PW],
                                                  const uint32_t (&boff)[B_PW], int kb, int klim,
@@ -189,14 +222,14 @@ __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, c
     if (bi >= a_blocks) continue;
     const int ch = (lane % CPR) ^ chunk_swz<BK>(bi * RPB + lane / CPR);
     const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
-    dma16((const bf16 *)(abase + (aoff[i] + (uint32_t)(off * 2))), st + bi * 1024);
+    dma16<DA>(abase, aoff[i] + (uint32_t)(off * 2), st + bi * 1024);
   }
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
     const int bi = wave * B_PW + i;
     const int ch = (lane % CPR) ^ chunk_swz<BK>(bi * RPB + lane / CPR);
     const int off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
-    dma16((const bf16 *)(bbase + (boff[i] + (uint32_t)(off * 2))), st + A_BYTES + bi * 1024);
+    dma16<DA>(bbase, boff[i] + (uint32_t)(off * 2), st + A_BYTES + bi * 1024);
   }
 }
 
@@ -273,14 +306,13 @@ __device__ __forceinline__ void issue_stage_kn(char *st, int wave, int lane, con
       const int ch = (lane % CPR) ^ chunk_swz<64>(bi * RPB + lane / CPR);
       off = (kb + ch * 8 < klim) ? kb : (klim - 8 - ch * 8);
     }
-    dma16((const bf16 *)(abase + (aoff[i] + (uint32_t)(off * 2))), st + bi * 1024);
+    dma16<true>(abase, aoff[i] + (uint32_t)(off * 2), st + bi * 1024);
   }
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
     const int kr = (wave * B_PW + i) * RPK + lane / (BN / 8);
     const int row = kb + kr < klim ? kb : klim - 1 - kr;    // row offset beyond kr
-    dma16((const bf16 *)(bbase + (boff[i] + (uint32_t)row * ldb2)),
-          st + A_BYTES + (wave * B_PW + i) * 1024);
+    dma16<true>(bbase, boff[i] + (uint32_t)row * ldb2, st + A_BYTES + (wave * B_PW + i) * 1024);
   }
 }
 
@@ -292,9 +324,6 @@ enum { B_BF16 = ART_MOE_B_BF16, B_FP8_ROWSCALE = ART_MOE_B_FP8_ROWSCALE,
 
 __device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
-__device__ __forceinline__ void dma16v(const void *g, void *lds) {
-  __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)lds, 16, 0, 0);
-}
 
 template <int A_PW, int B_PW8, int A_BYTES>
 __device__ __forceinline__ void issue_stage_b8(char *st, int wave, const char *abase,
@@ -303,10 +332,10 @@ __device__ __forceinline__ void issue_stage_b8(char *st, int wave, const char *a
                                                uint32_t sh_b) {
 #pragma unroll
   for (int i = 0; i < A_PW; ++i)
-    dma16((const bf16 *)(abase + (aoff[i] + sh_a)), st + (wave * A_PW + i) * 1024);
+    dma16<false>(abase, aoff[i] + sh_a, st + (wave * A_PW + i) * 1024);
 #pragma unroll
   for (int i = 0; i < B_PW8; ++i)
-    dma16v(bbase + (boff[i] + sh_b), st + A_BYTES + (wave * B_PW8 + i) * 1024);
+    dma16<false>(bbase, boff[i] + sh_b, st + A_BYTES + (wave * B_PW8 + i) * 1024);
 }
 
 // Eight e4m3fn weights -> bf16(q * scale): the dequantised weight of the
@@ -539,7 +568,7 @@ __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_l
 // chunk; epi_lora_proj zeroes those columns).  16-byte chunk c of row n goes
 // to physical chunk c ^ (n & 15), so the 16 rows a half-wave reads at one
 // column land on distinct banks.
-template <int KC, int NREG, int NW>
+template <int KC, int NREG, int NW, bool DA = false>
 __device__ __forceinline__ void load_proj_slice(char *pj_lds, const bf16 *P, int ldp,
                                                 const int (&pcol)[NREG], const int (&plim)[NREG],
                                                 int NQ, int wave, int lane) {
@@ -554,8 +583,7 @@ __device__ __forceinline__ void load_proj_slice(char *pj_lds, const bf16 *P, int
 #pragma unroll
     for (int gg = 0; gg < NREG; ++gg)
       if (gg == g) col = pcol[gg] + lc * 8 < plim[gg] ? pcol[gg] + lc * 8 : pcol[gg];
-    __builtin_amdgcn_global_load_lds((const void *)(P + (int64_t)n * ldp + col),
-                                     (lds_void_ptr)(pj_lds + ii * 1024), 16, 0, 0);
+    dma16<DA>((const char *)P, (uint32_t)(n * ldp + col) * 2u, pj_lds + ii * 1024);
   }
 }
 
@@ -764,7 +792,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       const uint32_t ch = (uint32_t)(dch ^ chunk_swz<BK>(r));                                 \
       loff_[i] = ((uint32_t)n * (uint32_t)p.ldl + ch * 8) * 2u;                               \
     }                                                                                         \
-    issue_stage_tail<A_PW, B_PW, A_BYTES, BK>(                                                \
+    issue_stage_tail<A_PW, B_PW, A_BYTES, BK, BKN>(                                           \
         smem + ((ks) % STAGES) * STAGE_BYTES, wave, lane, (const char *)p.t,                  \
         (const char *)(p.l + (int64_t)e * p.l_es), toff_, loff_, ((ks) - nk_main) * BK, p.kt, \
         a_blocks);                                                                            \
@@ -778,8 +806,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         issue_stage_b8<A_PW, B_PW8, A_BYTES>(st_, wave, abase, bbase, aoff, boff,             \
                                              (uint32_t)((ks) * BK * 2), (uint32_t)((ks) * BK)); \
         if (BQ8 == B_FP8_KSCALE && wave == 0 && lane < BK / 4)                                \
-          dma16v(p.b_scale + (int64_t)e * p.bs_es + (ks) * BK + lane * 4,                     \
-                 st_ + A_BYTES + B_BYTES);                                                    \
+          __builtin_amdgcn_global_load_lds(p.b_scale + (int64_t)e * p.bs_es + (ks) * BK + lane * 4, \
+                                           (lds_void_ptr)(st_ + A_BYTES + B_BYTES), 16, 0, 0); \
       } else if constexpr (BKN) {                                                             \
         issue_stage_kn<A_PW, B_PW, A_BYTES, BN, false>(st_, wave, lane, abase, bbase, aoff,   \
                                                        boff, (ks) * BK, p.K, ldb2, a_blocks); \
@@ -828,7 +856,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
                            PJ_NREG * p.pj_n * PJ_KC * 2 <= PJ_BYTES;
     if constexpr (EPI != EPI_STORE && PJ_KC >= 128) {
       if (pj_in_lds)
-        load_proj_slice<PJ_KC, PJ_NREG, NW>(pj_lds, p.pj_b + (int64_t)e * p.pj_es, p.pj_ld,
+        load_proj_slice<PJ_KC, PJ_NREG, NW, BKN>(pj_lds, p.pj_b + (int64_t)e * p.pj_es, p.pj_ld,
                                             pj_col, pj_lim, p.pj_n, wave, lane);
     }
 
