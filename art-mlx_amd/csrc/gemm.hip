@@ -247,13 +247,19 @@ __device__ __forceinline__ void issue_stage_tail(char *st, int wave, int lane, c
 typedef short kn_v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) kn_v4i16 *kn_lds_v4;
 
+// The lane's part of the address (row 8 lk + s / 4 of the k step, its
+// columns, the XOR) does not depend on kk: it is formed once, and the k step
+// adds a constant (kk * 16 rows) that the read takes as its immediate offset.
 template <int BN>
-__device__ __forceinline__ bf16x8 kn_frag(const char *stb, int kk, int col0, int lrow, int lk) {
+__device__ __forceinline__ int kn_lane_off(int col0, int lrow, int lk) {
   const int s = lrow & 15;
   const int col = col0 + 16 * (lrow >> 4) + 4 * (s & 3);
-  const int r = kk * 16 + 8 * lk + (s >> 2);              // r & 3 == s >> 2 (r % 8 < 4)
-  const int off = (((col >> 3) ^ ((s >> 2) << 2)) << 4) + ((col & 7) << 1);
-  const char *p = stb + r * (2 * BN) + off;
+  const int r = 8 * lk + (s >> 2);                         // r & 3 == s >> 2
+  return r * (2 * BN) + ((((col >> 3) ^ ((s >> 2) << 2)) << 4) + ((col & 7) << 1));
+}
+template <int BN>
+__device__ __forceinline__ bf16x8 kn_frag(const char *stb, int kk, int col0, int lrow, int lk) {
+  const char *p = (stb + kn_lane_off<BN>(col0, lrow, lk)) + kk * 16 * (2 * BN);
   kn_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((kn_lds_v4)p);
   kn_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((kn_lds_v4)(p + 4 * (2 * BN)));
   bf16x8 v;
@@ -1280,7 +1286,10 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
 // 15: 128x256 (2x4, 4)  16: 128x256 (2x4, 6)  17: 256x128 (4x2, 6)
 enum { kNumTileCfgs = 18 };
 // Defaults from a sweep of the C1 products on MI355X.
-enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 3 };
+// Default macro tiles (measured at C1).  The FC2 data gradient on a k-major W2
+// runs the 2-stage 128x256 tile: a third stage buys nothing there and costs
+// address arithmetic for the transposing reads of the extra stage slot.
+enum { kTileStore = 5, kTileSwigluFwd = 5, kTileSwigluBwd = 3, kTileSwigluBwdKn = 11 };
 
 template <int EPI>
 static int launch_big(int cfg, const NTArgs &p, const int32_t *seg, int64_t M, hipStream_t s,
@@ -1375,7 +1384,7 @@ static int swiglu_tile_cols(int product, int32_t fmt) {
   if (product == 0)
     return (fmt == ART_MOE_B_BF16 ? cfg_bn(tile_cfg(kTileSwigluFwd, "FC1")) : 256) / 2;
   if (fmt == ART_MOE_B_KN) {
-    const int c = kn_cfg(tile_cfg(kTileSwigluBwd, "BWD"));
+    const int c = kn_cfg(tile_cfg(kTileSwigluBwdKn, "BWD"));
     return c < 0 ? 256 : cfg_bn(c);
   }
   return fmt == ART_MOE_B_BF16 ? cfg_bn(tile_cfg(kTileSwigluBwd, "BWD")) : 256;
@@ -1637,7 +1646,7 @@ extern "C" int art_moe_fc2_dgrad_swiglu(const void *a, int64_t lda, const int32_
               pj_split, pj_n);
   p.pj_split = pj_b ? pj_split : 0;
   if (kn)
-    return launch_kn<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwd, "BWD"), p, seg, M,
+    return launch_kn<EPI_SWIGLU_BWD>(tile_cfg(kTileSwigluBwdKn, "BWD"), p, seg, M,
                                      as_stream(stream), "fc2_dgrad_swiglu/kn");
   if (w2_format != ART_MOE_B_BF16)
     return launch_fp8<EPI_SWIGLU_BWD>(w2_format, p, seg, M, as_stream(stream),

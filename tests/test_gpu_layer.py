@@ -311,9 +311,9 @@ def test_layer_fused_main_grad_accumulation(device, cfg_name):
 
 
 def test_layer_without_weight_copies_is_bit_identical(device):
-    """FrozenExperts without the transposed W2 copy (the FC2 data gradient
-    reads W2 k-major, as the FC1 one always reads W1) gives the same bits as
-    the default layer: same tiles, same k order."""
+    """FrozenExperts with the transposed W2 copy (row-major FC2 data
+    gradient, the default) and without it (W2 read k-major, as W1 always is)
+    give the same bits: same tile geometry, same k order."""
     from art_amd.megatron.moe_layer import FrozenExperts, moe_lora_layer
     print("layer without weight copies", flush=True)
     inp = _small("C1", 512)
