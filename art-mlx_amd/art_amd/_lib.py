@@ -83,6 +83,7 @@ SIGNATURES = {
                                      _SZ, _P]),
     "art_moe_wgrad_workspace_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
     "art_moe_wgrad_noalloc_scratch_bytes": (_SZ, []),
+    "art_moe_set_gemm_cu_reserve": (_I32, [_I32]),
     "art_moe_grouped_wgrad_noalloc": (_I32, [_P, _I64, _P, _P, _I64, _P, _P, _I32, _I64, _I32, _I32,
                                              _F, _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64,
                                              _I32, _P]),

@@ -6,6 +6,7 @@ current stream.  No function synchronizes with the host.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from dataclasses import dataclass
 
@@ -473,6 +474,17 @@ def grouped_wgrad(lm: torch.Tensor, r: torch.Tensor, seg: torch.Tensor, num_expe
          ptr(out2), int(q_split), o2_es, o2_ps, o2_qs, mode, ptr(ws), ws_bytes,
          stream_ptr(lm.device))
     return out
+
+
+@contextlib.contextmanager
+def gemm_cu_reserve(cus: int):
+    """Grouped products launched inside the block (from this host thread)
+    leave ``cus`` compute units free for kernels on other streams; 0 after."""
+    call("art_moe_set_gemm_cu_reserve", int(cus))
+    try:
+        yield
+    finally:
+        call("art_moe_set_gemm_cu_reserve", 0)
 
 
 def transpose_into(src: torch.Tensor, dst: torch.Tensor, scale: float = 1.0) -> torch.Tensor:

@@ -1252,6 +1252,10 @@ static int tile_sched(int epi) {
   return v[epi];
 }
 
+// Compute units the persistent products leave free for work on other streams
+// (art_moe_set_gemm_cu_reserve; per host thread).
+static thread_local int g_cu_reserve = 0;
+
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64,
           bool F16 = false>
 static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t s,
@@ -1275,7 +1279,7 @@ static int launch_nt(const NTArgs &a, const int32_t *seg, int64_t M, hipStream_t
   p.sched = tile_sched(EPI);
   const int n_tiles = (a.N + BN - 1) / BN;
   const int64_t max_tiles = ((M + BM - 1) / BM + a.E) * (int64_t)n_tiles;
-  int64_t grid = (int64_t)device_cu_count() * occ;
+  int64_t grid = (int64_t)(device_cu_count() - g_cu_reserve) * occ;
   if (grid > max_tiles) grid = max_tiles;
   if (grid >= 8) grid &= ~(int64_t)7;
   if (grid < 1) grid = 1;
@@ -1421,6 +1425,13 @@ __global__ __launch_bounds__(256) void sum_parts_kernel(const float *__restrict_
 using namespace art;
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int art_moe_set_gemm_cu_reserve(int32_t cus) {
+  const int n = device_cu_count();
+  ART_REQUIRE(cus >= 0 && cus <= n / 2, "set_gemm_cu_reserve: %d CUs (0 .. %d)", cus, n / 2);
+  g_cu_reserve = cus;
+  return ART_MOE_OK;
+}
 
 extern "C" int art_moe_lora_epilogue_parts(int32_t product, int32_t F, int32_t w_format) {
   if (F <= 0 || (product != 0 && product != 1)) return 0;

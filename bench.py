@@ -141,13 +141,17 @@ def gpu_bench(cfg, steps: int, warmup: int, seed: int = 0, w8a8: bool = False):
     timer.enabled = False
     tot_fc1, cnt_fc1 = timer.collect()
     # Per-op breakdown: the same steps again with every op bracketed, outside
-    # the timed region (diagnostic fields only).
+    # the timed region (diagnostic fields only), without the weight-gradient
+    # overlap so that each op's time is its own.
+    overlap = moe_layer.OVERLAP_WGRAD_CUS
+    moe_layer.OVERLAP_WGRAD_CUS = 0
     timer.only = None
     timer.enabled = True
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     timer.enabled = False
+    moe_layer.OVERLAP_WGRAD_CUS = overlap
     tot, cnt = timer.collect()
     return (t1 - t0) * 1e3 / steps, (tot_fc1, cnt_fc1), (tot, cnt)
 

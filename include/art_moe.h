@@ -361,6 +361,13 @@ size_t art_moe_wgrad_workspace_bytes(int64_t M, int32_t E, int32_t P, int32_t Q)
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid allocation). */
 size_t art_moe_wgrad_noalloc_scratch_bytes(void);
+
+/* Compute units (0 .. half the device's) that the persistent grouped
+ * products launched afterwards from the calling host thread leave free, so
+ * that kernels on another stream run beside them; 0 (the default) sizes their
+ * grid to every CU.  Results do not depend on it.  No counterpart in the
+ * reference (a scheduling control of this build). */
+int art_moe_set_gemm_cu_reserve(int32_t cus);
 int art_moe_grouped_wgrad_noalloc(const void *lm, int64_t ldl, const int32_t *l_rows,
                                   const void *r, int64_t ldr, const int32_t *r_rows,
                                   const int32_t *seg, int32_t E, int64_t M, int32_t P,

@@ -332,3 +332,39 @@ def test_layer_without_weight_copies_is_bit_identical(device):
         outs.append([y.detach(), x.grad] + [lora[n].grad for n in NAMES])
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+def test_layer_wgrad_overlap_is_bit_identical(device):
+    """The backward with the LoRA weight gradients on a side stream (the data
+    gradients on a reduced persistent grid) gives the same bits as the
+    single-stream backward, with the fp32 main_grad landing as well."""
+    from art_amd.megatron import moe_layer
+    print("layer wgrad overlap", flush=True)
+    inp = _small("C1", 2048)
+    base = moe_layer.FrozenExperts.build(inp.w_r.to(device), inp.w1.to(device),
+                                         inp.w2.to(device))
+    saved = moe_layer.OVERLAP_WGRAD_CUS
+    outs = []
+    try:
+        for cus in (0, 32, 0, 32):
+            moe_layer.OVERLAP_WGRAD_CUS = cus
+            lora = {n: inp.lora[n].to(device).requires_grad_() for n in NAMES}
+            fuse = len(outs) >= 2
+            if fuse:
+                for v in lora.values():
+                    v.main_grad = torch.zeros(v.shape, dtype=torch.float32, device=device)
+            x = inp.x.to(device).requires_grad_()
+            s = inp.cfg.scale
+            y, _, _, _ = moe_layer.moe_lora_layer(x, base, *(lora[n] for n in NAMES),
+                                                  k=inp.cfg.k, scales=(s, s, s),
+                                                  fuse_main_grad=fuse)
+            y.backward(inp.dy.to(device))
+            torch.cuda.synchronize()
+            g = [lora[n].main_grad if fuse else lora[n].grad for n in NAMES]
+            outs.append([y.detach(), x.grad] + g)
+    finally:
+        moe_layer.OVERLAP_WGRAD_CUS = saved
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+    for a, b in zip(outs[2], outs[3]):
+        assert torch.equal(a, b)
