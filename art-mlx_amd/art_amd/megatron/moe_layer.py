@@ -55,11 +55,20 @@ FUSE_MAX_WIDTH_FWD, FUSE_MAX_WIDTH_BWD = 16, 32
 # Backward: with OVERLAP_WGRAD_CUS = n > 0 the LoRA weight-gradient products
 # (HBM-bound) run on a side stream beside the FC2 and FC1 data gradients
 # (MFMA-bound), which then leave n compute units free; 0 runs everything on
-# the caller's stream (ART_MOE_OVERLAP_WGRAD overrides).  Measured per step:
-# C1 -2%, C2 -2.7%, C3 -3% with 32 (16 and 48 lose to tile-round quantisation
-# of the persistent grids).
+# the caller's stream (ART_MOE_OVERLAP_WGRAD overrides).  It pays when the
+# weight gradients' traffic is large next to the data gradients' work, which
+# the reserved CUs slow down by more than n / CUs (tile rounds quantise):
+# measured per step with 32, C1 -2%, C2 -2.7%, C3 -3%, but C4 (H = 4096,
+# F = 1536) +2.5%; 16 and 48 lose everywhere.
 OVERLAP_WGRAD_CUS = int(os.environ.get("ART_MOE_OVERLAP_WGRAD", "32"))
 _SIDE_STREAMS: dict = {}
+
+
+def _overlap_pays(hidden: int, ffn: int) -> bool:
+    """Weight-gradient bytes per data-gradient FLOP, ~(2H + 3F) / (H F) up to
+    constants: 4.1e-3 at C1-C3's H = 2048, F = 768 (overlap measured faster),
+    2.0e-3 at C4's 4096 / 1536 (slower)."""
+    return (2 * hidden + 3 * ffn) / (hidden * ffn) >= 3.0e-3
 
 
 def _side_stream(device) -> torch.cuda.Stream:
@@ -340,7 +349,7 @@ class _MoELoRALayerFn(torch.autograd.Function):
         # FC2 data gradient with the SwiGLU backward in its epilogue
         g2 = ops.grouped_gemm(dy, bdp, seg, e, m=m, a_rows=rows, alpha=sd)
         fuse = ctx.fuse_main_grad
-        ov = OVERLAP_WGRAD_CUS
+        ov = OVERLAP_WGRAD_CUS if _overlap_pays(h_dim, f) else 0
         main = torch.cuda.current_stream(dy.device)
         side = _side_stream(dy.device) if ov else None
 
