@@ -147,9 +147,21 @@ class FrozenExperts:
         return self.w1.shape[1] // 2
 
 
+_ONE_SEGMENT: dict = {}
+
+
 def _single_segment(num_rows: int, device) -> torch.Tensor:
-    counts = torch.full((1,), num_rows, dtype=torch.int64, device=device)
-    return ops.segments_from_counts(counts, 1, device)
+    """The segment table of one expert owning all rows (read-only, cached per
+    device and row count; a table first built under graph capture is not
+    cached, since its contents are written only when the graph replays)."""
+    key = (torch.device(device).index, int(num_rows))
+    seg = _ONE_SEGMENT.get(key)
+    if seg is None:
+        counts = torch.full((1,), num_rows, dtype=torch.int64, device=device)
+        seg = ops.segments_from_counts(counts, 1, device)
+        if not torch.cuda.is_current_stream_capturing():
+            _ONE_SEGMENT[key] = seg
+    return seg
 
 
 def router_logits(x: torch.Tensor, w_r: torch.Tensor, seg: torch.Tensor | None = None,
@@ -196,11 +208,13 @@ def _land_wgrad(lm, r, seg, e, targets, *, alpha=1.0, l_rows=None, transpose_out
     kw = dict(alpha=alpha, l_rows=l_rows, transpose_out=transpose_out)
     ranks = [_rank_of(p, transpose_out) for p, _ in targets]
     mgs = [getattr(p, "main_grad", None) for p, _ in targets]
+    q0s = [q0 for _, q0 in targets]
+    # the product's columns are exactly the targets' (no rank padding): the
+    # kernel writes each target's gradient in place (out / out2)
+    exact = (len(targets) == 1 and q0s[0] == 0 and ranks[0] == q) or (
+        len(targets) == 2 and q0s[0] == 0 and ranks[0] == q0s[1] and q0s[1] + ranks[1] == q)
     if fuse_main_grad and all(mg is not None and mg.dtype == torch.float32 and mg.shape == p.shape
                               for mg, (p, _) in zip(mgs, targets)):
-        q0s = [q0 for _, q0 in targets]
-        exact = (len(targets) == 1 and q0s[0] == 0 and ranks[0] == q) or (
-            len(targets) == 2 and q0s[0] == 0 and ranks[0] == q0s[1] and q0s[1] + ranks[1] == q)
         if exact:
             ops.grouped_wgrad(lm, r, seg, e, out=_as3(mgs[0]), accumulate=True,
                               out2=_as3(mgs[1]) if len(targets) == 2 else None,
@@ -213,6 +227,11 @@ def _land_wgrad(lm, r, seg, e, targets, *, alpha=1.0, l_rows=None, transpose_out
             p.grad_added_to_main_grad = True
         return [None] * len(targets)
     od = torch.bfloat16 if targets[0][0].dtype == torch.bfloat16 else torch.float32
+    if exact:   # contiguous, parameter-shaped gradients (no copy when autograd lands them)
+        outs = [torch.empty(_as3(p).shape, dtype=od, device=lm.device) for p, _ in targets]
+        ops.grouped_wgrad(lm, r, seg, e, out=outs[0], out2=outs[1] if len(outs) == 2 else None,
+                          q_split=q0s[1] if len(outs) == 2 else 0, **kw)
+        return [(o if p.dim() == 3 else o[0]).to(p.dtype) for o, (p, _) in zip(outs, targets)]
     full = ops.grouped_wgrad(lm, r, seg, e, out_dtype=od, **kw)
     grads = []
     for (p, q0), rk in zip(targets, ranks):
@@ -311,6 +330,8 @@ class _MoELoRALayerFn(torch.autograd.Function):
         ctx.logits_supplied = logits_supplied
         ctx.fuse_main_grad = fuse_main_grad
         ctx.mark_non_differentiable(idx, plan.counts, status)
+        # no zero gradients for the integer outputs (three fill kernels a step)
+        ctx.set_materialize_grads(False)
         return y, idx, plan.counts, status
 
     @staticmethod
@@ -322,7 +343,7 @@ class _MoELoRALayerFn(torch.autograd.Function):
         e, f = base.num_experts, base.ffn
         t = x.shape[0]
         m = t * k
-        dy = dy.contiguous()
+        dy = torch.zeros_like(x) if dy is None else dy.contiguous()
         h_dim = base.hidden
         # backward operand layouts in one launch: B_d and A_d rank-padded, the
         # block-diagonal [[s_g B_g, 0], [0, s_u B_u]] (g1 = [s_g dg B_g^T | s_u du B_u^T]
