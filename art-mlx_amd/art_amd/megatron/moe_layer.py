@@ -160,6 +160,8 @@ def _single_segment(num_rows: int, device) -> torch.Tensor:
         counts = torch.full((1,), num_rows, dtype=torch.int64, device=device)
         seg = ops.segments_from_counts(counts, 1, device)
         if not torch.cuda.is_current_stream_capturing():
+            if len(_ONE_SEGMENT) >= 64:   # varying token counts: keep the cache small
+                _ONE_SEGMENT.clear()
             _ONE_SEGMENT[key] = seg
     return seg
 
