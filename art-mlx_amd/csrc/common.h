@@ -41,8 +41,15 @@ int device_cu_count();
 __device__ __forceinline__ float bf16_to_f(bf16 v) { return (float)v; }
 __device__ __forceinline__ bf16 f_to_bf16(float v) { return (bf16)v; }
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
-__device__ __forceinline__ float sigmoid_f(float g) { return 1.0f / (1.0f + __expf(-g)); }
+// sigmoid through v_rcp_f32 (within 1 ulp) instead of a correctly rounded divide: the
+// divide's scale / refine / fixup sequence was half of the SwiGLU epilogues' vector
+// instructions, and the difference stays far below the bf16 rounding of every output.
+// Limits match the divide: g -> +inf gives 1 (silu g), g -> -inf gives 0 (silu -0), NaN
+// stays NaN.
+__device__ __forceinline__ float sigmoid_f(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 

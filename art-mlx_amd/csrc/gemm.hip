@@ -1079,6 +1079,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       }
     } else if (EPI == EPI_SWIGLU_FWD) {
       const int F = p.F;
+      // The routing weights of the rows this thread finishes in pass 2, loaded
+      // before pass 1 so that their latency hides under the staging: a load
+      // inside pass 2 would be followed by a vmcnt(0) wait, which on gfx9 also
+      // waits for the y1 / h stores just issued, once per iteration.
+      constexpr int P2_IT = BM * (BN / 16) / NT;
+      static_assert(BM * (BN / 16) % NT == 0, "pass 2 splits evenly over the threads");
+      float prv[P2_IT];
+#pragma unroll
+      for (int it = 0; it < P2_IT; ++it) {
+        const int m = m0 + (tid + it * NT) / (BN / 16);
+        prv[it] = m < m_end ? p.prob[m] : 0.0f;
+      }
       // pass 1: gate and up rounded to bf16, staged per 64-column physical
       // block as [32 gate | 32 up] (units ug .. ug+7 gate, ug+8 .. ug+15 up)
 #pragma unroll
@@ -1101,7 +1113,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       // h = silu(g) * u * p from the same bf16 values, out and back into the
       // gate chunk's units (the LoRA projection below reads h there; columns
       // past F and rows past the segment hold zeros)
-      for (int idx = tid; idx < BM * (BN / 16); idx += NT) {
+#pragma unroll
+      for (int it = 0; it < P2_IT; ++it) {
+        // addresses formed here, not hoisted out of the tile loop: kept live
+        // across the k-loop they spill, and each spill reload is a vector
+        // memory load whose wait drains this loop's stores
+        int idx = tid + it * NT;
+        asm volatile("" : "+v"(idx));
         const int row = idx / (BN / 16), ch = idx - row * (BN / 16);
         const int gch = (ch >> 2) * 8 + (ch & 3);        // gate chunk; up chunk gch + 4
         const U4 g8 = load_chunk(row, gch), u8 = load_chunk(row, gch + 4);
@@ -1113,7 +1131,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
           bf16 *y = p.y1 + (int64_t)m * (2 * F) + f;
           *(U4 *)y = g8;
           *(U4 *)(y + F) = u8;
-          const float pr = p.prob[m];
+          const float pr = prv[it];
           const uint32_t gw[4] = {g8.x, g8.y, g8.z, g8.w}, uw[4] = {u8.x, u8.y, u8.z, u8.w};
           uint32_t hw[4];
 #pragma unroll
