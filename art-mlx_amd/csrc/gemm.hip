@@ -536,6 +536,16 @@ __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_l
       if (g < g_lo || g >= g_hi) continue;
       const int r = g * REG_ROWS + rb * 16 + l16;
       const char *brow = pj_lds ? pj_lds + (g * NQ + n) * (KC * 2) : nullptr;
+      // operand rows read from global memory: all KS loads issued before
+      // the first MFMA (one round trip, not one per k-step pair)
+      U4 bg[KS];
+      if (!brow) {
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          const int c = pcol[g] + kk * 32 + 8 * g4;
+          bg[kk] = *(const U4 *)(prow + (c < plim[g] ? c : pcol[g]));
+        }
+      }
 #pragma unroll
       for (int k0 = 0; k0 < KS; k0 += 2) {
         U4 a4[2], b4[2];
@@ -549,7 +559,7 @@ __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_l
           a4[j] = U4{lo.x, lo.y, hi.x, hi.y};
           const int c = pcol[g] + kk * 32 + 8 * g4;
           if (brow) b4[j] = *(const U4 *)(brow + (((kk * 4 + g4) ^ (n & 15)) << 4));
-          else b4[j] = *(const U4 *)(prow + (c < plim[g] ? c : pcol[g]));
+          else b4[j] = bg[kk];
           if (c >= plim[g]) b4[j] = U4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
@@ -1174,16 +1184,45 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
           const int m = m0 + row;
           const int mc = m < m_end ? m : m_end - 1;
           const float pr = p.prob[mc];
-          const bf16 *yr = p.y1_in + (int64_t)mc * (2 * F);
+          {
+            // y1 of the wave's 32-row block, read coalesced (WTN/8 lanes per
+            // row, 16 bytes each; a per-lane 8-byte read in the MFMA layout
+            // touches 32 rows per instruction) into the wave's own units of
+            // the two staging regions.  Each lane then reads its g / u units
+            // back and overwrites them with dg / du: every unit has one
+            // reader, which is also its only writer after the copy.
+            constexpr int LPR = WTN / 8, RPI = 64 / LPR, NI = 32 / RPI;
+            static_assert(LPR >= 1 && 64 % LPR == 0 && 32 % RPI == 0, "y1 block copy");
+#pragma unroll
+            for (int reg = 0; reg < 2; ++reg) {   // gate, then up (16 VGPRs in flight)
+              U4 yl[NI];
+#pragma unroll
+              for (int t = 0; t < NI; ++t) {
+                const int rr = t * RPI + lane / LPR, c8 = lane % LPR;
+                const int mg = m0 + wm * WTM + i * 32 + rr;
+                const int fg0 = nt * BN + wn * WTN + 8 * c8;
+                yl[t] = *(const U4 *)(p.y1_in + (int64_t)(mg < m_end ? mg : m_end - 1) * (2 * F) +
+                                      reg * F + (fg0 < F ? fg0 : 0));
+              }
+#pragma unroll
+              for (int t = 0; t < NI; ++t) {
+                const int rr = t * RPI + lane / LPR, c8 = lane % LPR;
+                const int lrr = reg * RG + wm * WRG + ii * 32 + rr;
+                const int u0 = (wn * WTN) / 4 + 2 * c8;
+                stage_unit(lrr, u0, uint2{yl[t].x, yl[t].y});
+                stage_unit(lrr, u0 + 1, uint2{yl[t].z, yl[t].w});
+              }
+            }
+          }
 #pragma unroll
           for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              int f = nt * BN + wn * WTN + j * 32 + 8 * q + 4 * lk;
+              const int f = nt * BN + wn * WTN + j * 32 + 8 * q + 4 * lk;
               const bool fin = f < F;
-              f = fin ? f : 0;
-              const uint2 gr = *(const uint2 *)(yr + f);
-              const uint2 ur = *(const uint2 *)(yr + F + f);
+              const int unit = (wn * WTN + j * 32) / 4 + 2 * q + lk;
+              const uint2 gr = stg[lr * UPR + (unit ^ (lr & UMASK))];
+              const uint2 ur = stg[(RG + lr) * UPR + (unit ^ ((RG + lr) & UMASK))];
               const float g4[4] = {__uint_as_float(gr.x << 16), __uint_as_float(gr.x & 0xffff0000u),
                                    __uint_as_float(gr.y << 16), __uint_as_float(gr.y & 0xffff0000u)};
               const float u4[4] = {__uint_as_float(ur.x << 16), __uint_as_float(ur.x & 0xffff0000u),
@@ -1199,13 +1238,23 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
                 du[v] = dhp * sl;
                 if (fin) rs[i] += dh * sl * u4[v];
               }
-              const int unit = (wn * WTN + j * 32) / 4 + 2 * q + lk;
               stage_unit(lr, unit, pack4(dg[0], dg[1], dg[2], dg[3]));
               stage_unit(RG + lr, unit, pack4(du[0], du[1], du[2], du[3]));
             }
           rs[i] += __shfl_xor(rs[i], 32, kWave);  // lanes l and l+32 share the row
         }
         barrier_nofence();
+        // fused LoRA projection of dy1 = [dg | du]: g1 partial of this column
+        // tile (dg against P columns f, du against P columns F + f).  Ahead of
+        // the dy1 stores: its operand loads, when they come from global
+        // memory, would otherwise wait for those stores to drain.
+        if constexpr (EPI == EPI_SWIGLU_BWD) if (p.pj_b) {
+          epi_lora_proj<BN, UPR, UMASK, 8, 2, RG, RG, NW>(
+              stg, (PJ_KC >= 128 && pj_in_lds) ? pj_lds : nullptr, p.pj_b + (int64_t)e * p.pj_es,
+              p.pj_ld, pj_col, pj_lim, p.pj_n, p.pj_split,
+              p.pj_part + (int64_t)nt * p.M * p.pj_n, p.M, m0, m_end, wave, lane,
+              [&](int lr) { return (lr / WRG) * WTM + h * WRG + (lr % WRG); });
+        }
         // dg -> dy1[:, f], du -> dy1[:, F + f] for the group's rows
         for (int idx = tid; idx < 2 * RG * (BN / 8); idx += NT) {
           const int region = idx / (RG * (BN / 8));
@@ -1215,15 +1264,6 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
           const int m = m0 + row, f = nt * BN + ch * 8;
           if (m < m_end && f < F)
             *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + region * F + f) = load_chunk(region * RG + lr, ch);
-        }
-        // fused LoRA projection of dy1 = [dg | du]: g1 partial of this column
-        // tile (dg against P columns f, du against P columns F + f)
-        if constexpr (EPI == EPI_SWIGLU_BWD) if (p.pj_b) {
-          epi_lora_proj<BN, UPR, UMASK, 8, 2, RG, RG, NW>(
-              stg, (PJ_KC >= 128 && pj_in_lds) ? pj_lds : nullptr, p.pj_b + (int64_t)e * p.pj_es,
-              p.pj_ld, pj_col, pj_lim, p.pj_n, p.pj_split,
-              p.pj_part + (int64_t)nt * p.M * p.pj_n, p.M, m0, m_end, wave, lane,
-              [&](int lr) { return (lr / WRG) * WTM + h * WRG + (lr % WRG); });
         }
         if (h + 1 < EPI2_NH) barrier_nofence();  // the next group reuses the regions
       }
