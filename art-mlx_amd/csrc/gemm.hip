@@ -535,7 +535,8 @@ __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_l
     for (int g = 0; g < NREG; ++g) {
       if (g < g_lo || g >= g_hi) continue;
       const int r = g * REG_ROWS + rb * 16 + l16;
-      const char *brow = pj_lds ? pj_lds + (g * NQ + n) * (KC * 2) : nullptr;
+      const int srow = (NREG > 1 && split > 0) ? n : g * NQ + n;   // row in the LDS slice
+      const char *brow = pj_lds ? pj_lds + srow * (KC * 2) : nullptr;
       // operand rows read from global memory: all KS loads issued before
       // the first MFMA (one round trip, not one per k-step pair)
       U4 bg[KS];
@@ -581,19 +582,22 @@ __device__ __forceinline__ void epi_lora_proj(const uint2 *stg, const char *pj_l
 
 // The tile's slice of the projection operand into LDS by DMA: region g,
 // row n, columns pcol[g] .. +KC (chunks past the row's end re-read its first
-// chunk; epi_lora_proj zeroes those columns).  16-byte chunk c of row n goes
-// to physical chunk c ^ (n & 15), so the 16 rows a half-wave reads at one
-// column land on distinct banks.
+// chunk; epi_lora_proj zeroes those columns), at slice row g * NQ + n; with a
+// block-diagonal operand (split > 0) only the region each row reads, at
+// slice row n.  16-byte chunk c of row n goes to physical chunk c ^ (n & 15),
+// so the 16 rows a half-wave reads at one column land on distinct banks.
 template <int KC, int NREG, int NW, bool DA = false>
 __device__ __forceinline__ void load_proj_slice(char *pj_lds, const bf16 *P, int ldp,
                                                 const int (&pcol)[NREG], const int (&plim)[NREG],
-                                                int NQ, int wave, int lane) {
+                                                int NQ, int split, int wave, int lane) {
   constexpr int CPRO = KC / 8;                         // chunks per row
-  const int n_instr = NREG * NQ * CPRO / 64;           // 1 KB per DMA instruction
+  const bool diag = NREG > 1 && split > 0;
+  const int n_instr = (diag ? NQ : NREG * NQ) * CPRO / 64;   // 1 KB per DMA instruction
   for (int ii = wave; ii < n_instr; ii += NW) {
     const int ch = ii * 64 + lane;                     // physical chunk index in the slice
-    const int row = ch / CPRO, pc = ch - row * CPRO;   // row = g * NQ + n
-    const int g = row / NQ, n = row - g * NQ;
+    const int row = ch / CPRO, pc = ch - row * CPRO;
+    const int g = diag ? ((row & ~15) >= split ? 1 : 0) : row / NQ;
+    const int n = diag ? row : row - g * NQ;
     const int lc = pc ^ (n & 15);
     int col = pcol[0];
 #pragma unroll
@@ -624,7 +628,14 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   // conservative for both (the per-k scale DMA of wave 0 likewise).
   constexpr int G = W8 ? A_PW + B_PW8 : A_PW + B_PW;
   constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
-  constexpr int RED_BYTES = EPI == EPI_SWIGLU_BWD ? WN * BM * 4 : 0;  // dp row partials
+  constexpr int EPI2_NH = EPI == EPI_SWIGLU_BWD ? epi2_groups(TM, BM, BN, LDS_BYTES) : 1;
+  // dp row partials of the SwiGLU backward: in the ring behind the staged dg
+  // and du where they fit (the ring is idle in the epilogue), else after it
+  constexpr int RED_NEED = EPI == EPI_SWIGLU_BWD ? WN * BM * 4 : 0;
+  constexpr int STG_BYTES = (EPI == EPI_SWIGLU_BWD && EPI2_NH >= 1) ? 4 * (BM / EPI2_NH) * BN : 0;
+  constexpr bool RED_IN_RING = RED_NEED > 0 && EPI2_NH >= 1 && STG_BYTES + RED_NEED <= LDS_BYTES;
+  constexpr int RED_BYTES = RED_IN_RING ? 0 : RED_NEED;
+  constexpr int RED_OFF = RED_IN_RING ? STG_BYTES : LDS_BYTES;
   // SwiGLU products with one workgroup per CU anyway: what LDS is left holds
   // the tile's slice of the LoRA projection operand (DMA'd with the first
   // stages, read by the epilogue)
@@ -642,7 +653,6 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
   static_assert(G * (STAGES - 2) <= 63 && STAGES >= 2 && STAGES <= 6, "vmcnt range");
   static_assert(LDS_BYTES + RED_BYTES + PJ_BYTES <= 160 * 1024, "LDS of one workgroup");
   static_assert(EPI != EPI_SWIGLU_BWD || (WTN <= 128 && 128 % WTN == 0), "dp partial groups");
-  constexpr int EPI2_NH = EPI == EPI_SWIGLU_BWD ? epi2_groups(TM, BM, BN, LDS_BYTES) : 1;
   static_assert(EPI2_NH >= 1, "SwiGLU backward staging (dg and du of a row group) must fit the LDS ring");
   static_assert(!W8 || (BN / 16) % NW == 0, "fp8 B DMA blocks must split across waves");
   static_assert(!F16 || (EPI == EPI_STORE && BQ8 == B_BF16), "fp16 operands: plain store products");
@@ -650,7 +660,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
                 "k-major B: 64-wide k-tiles, BN >= 128, data-gradient products");
 
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES + RED_BYTES + PJ_BYTES];
-  float *sRed = (float *)(smem + LDS_BYTES);
+  float *sRed = (float *)(smem + RED_OFF);
   char *pj_lds = smem + LDS_BYTES + RED_BYTES;
 
   // The wave index is uniform across the wave: readfirstlane tells the
@@ -868,12 +878,13 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
       pj_col[0] = nt * (BN / 2);
       pj_lim[0] = p.F;
     }
-    const bool pj_in_lds = EPI != EPI_STORE && p.pj_b &&
-                           PJ_NREG * p.pj_n * PJ_KC * 2 <= PJ_BYTES;
+    // a block-diagonal operand (pj_split > 0) keeps one region per row
+    const int pj_rows = (PJ_NREG > 1 && p.pj_split > 0) ? p.pj_n : PJ_NREG * p.pj_n;
+    const bool pj_in_lds = EPI != EPI_STORE && p.pj_b && pj_rows * PJ_KC * 2 <= PJ_BYTES;
     if constexpr (EPI != EPI_STORE && PJ_KC >= 128) {
       if (pj_in_lds)
         load_proj_slice<PJ_KC, PJ_NREG, NW, BKN>(pj_lds, p.pj_b + (int64_t)e * p.pj_es, p.pj_ld,
-                                            pj_col, pj_lim, p.pj_n, wave, lane);
+                                            pj_col, pj_lim, p.pj_n, p.pj_split, wave, lane);
     }
 
     // Wait until stage ks has landed (at most min(STAGES-2, nk-1-ks) later
