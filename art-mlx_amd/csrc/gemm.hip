@@ -607,6 +607,16 @@ __device__ __forceinline__ void load_proj_slice(char *pj_lds, const bf16 *P, int
   }
 }
 
+// Streaming (non-temporal) 16-byte store for the epilogue outputs: they are
+// read by later kernels, not by this one, and marked nt they do not displace
+// the operand panels the next tile's k-loop re-reads from L2 (FC1 -2%, the
+// plain-store products -1% at C1).
+__device__ __forceinline__ void store_nt(void *p, U4 v) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, (u32x4 *)p);
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, int EPI, int BQ8 = B_BF16, int BK = 64,
           bool F16 = false>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
@@ -1095,7 +1105,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         for (int idx = tid; idx < BM * (BN / 8); idx += NT) {
           const int row = idx / (BN / 8), ch = idx - row * (BN / 8);
           const int m = m0 + row, n = nt * BN + ch * 8;
-          if (m < m_end && n < p.N) *(U4 *)(c + (int64_t)m * p.ldc + n) = load_chunk(row, ch);
+          if (m < m_end && n < p.N) store_nt(c + (int64_t)m * p.ldc + n, load_chunk(row, ch));
         }
       }
     } else if (EPI == EPI_SWIGLU_FWD) {
@@ -1150,8 +1160,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
         U4 h8 = U4{0u, 0u, 0u, 0u};
         if (ok) {
           bf16 *y = p.y1 + (int64_t)m * (2 * F) + f;
-          *(U4 *)y = g8;
-          *(U4 *)(y + F) = u8;
+          store_nt(y, g8);
+          store_nt(y + F, u8);
           const float pr = prv[it];
           const uint32_t gw[4] = {g8.x, g8.y, g8.z, g8.w}, uw[4] = {u8.x, u8.y, u8.z, u8.w};
           uint32_t hw[4];
@@ -1162,7 +1172,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
             hw[w] = pack2(silu_f(g0) * u0 * pr, silu_f(g1) * u1 * pr);
           }
           h8 = U4{hw[0], hw[1], hw[2], hw[3]};
-          *(U4 *)(p.h + (int64_t)m * F + f) = h8;
+          store_nt(p.h + (int64_t)m * F + f, h8);
         }
         stage_unit(row, 2 * gch, uint2{h8.x, h8.y});
         stage_unit(row, 2 * gch + 1, uint2{h8.z, h8.w});
@@ -1274,7 +1284,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_nt_kernel(const NTArgs p) {
           const int row = (lr / WRG) * WTM + h * WRG + (lr % WRG);
           const int m = m0 + row, f = nt * BN + ch * 8;
           if (m < m_end && f < F)
-            *(U4 *)(p.dy1 + (int64_t)m * (2 * F) + region * F + f) = load_chunk(region * RG + lr, ch);
+            store_nt(p.dy1 + (int64_t)m * (2 * F) + region * F + f, load_chunk(region * RG + lr, ch));
         }
         if (h + 1 < EPI2_NH) barrier_nofence();  // the next group reuses the regions
       }
