@@ -124,10 +124,17 @@ def test_fc1_swiglu(device, e, m, f, h, kt, gather):
     assert rel(hh, h_ref) < 1e-2
 
 
-@pytest.mark.parametrize("e,m,f,h,kt", [(8, 1000, 512, 256, 16), (128, 4096, 768, 2048, 16)])
-def test_fc2_dgrad_swiglu(device, e, m, f, h, kt):
+@pytest.mark.parametrize("e,m,f,h,kt,tile", [
+    (8, 1000, 512, 256, 16, None), (128, 4096, 768, 2048, 16, None),
+    (8, 1000, 512, 256, 16, "5"),   # 256 x 256: the epilogue in two row groups
+    (8, 1000, 520, 256, 16, "6"),   # 4 x 2 waves: 128-column wave tiles, two row groups
+    (8, 1000, 512, 256, 16, "1"),   # 128 x 256 with 2 x 2 waves: 128-column wave tiles
+])
+def test_fc2_dgrad_swiglu(device, e, m, f, h, kt, tile, monkeypatch):
+    if tile is not None:
+        monkeypatch.setenv("ART_MOE_GEMM_TILE_BWD", tile)
     ops = _ops()
-    print(f"fc2_dgrad_swiglu e={e} m={m} f={f} h={h}", flush=True)
+    print(f"fc2_dgrad_swiglu e={e} m={m} f={f} h={h} tile={tile}", flush=True)
     g = torch.Generator().manual_seed(12)
     counts = _counts(e, m, seed=4)
     t_src = 600
