@@ -90,7 +90,7 @@ class FrozenExperts:
     transposing LDS reads, as fast as a transposed copy), so there is no W1
     copy (w1t None).  The FC2 data gradient keeps a transposed W2 copy
     w2t [E, F, H] by default: read k-major, its 64x64 wave tiles issue 1.5x
-    the LDS reads and the product takes ~12% longer (~45 us per C1 step).
+    the LDS reads and the product takes ~16% longer (~55 us per C1 step).
     ``build(..., w2_copy=False)`` drops the copy (the frozen weights then
     take no extra memory; results are bit-identical).
     With fp8 storage (``build_fp8``) w1 / w2 hold e4m3fn bytes with w1_scale
